@@ -1,0 +1,297 @@
+"""Benchmark: the MoE forward layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config fine_grained] [--routing random]
+
+Workload (default): the fine-grained layer, T=4096 tokens, D=1024, F=4096,
+E=64 experts, top-2, bf16, uniform routing (2 distinct experts per token),
+x ~ N(0,1), W1/W2 ~ N(0, 1/fan_in), softmax gates; synthetic, seeded.
+
+A step is one whole layer (routing -> SDD+GELU -> DSD -> combine) replayed
+from a HIP graph captured once, with inputs resident in HBM. Before each
+step a 512 MiB buffer is zeroed (outside the step's events) so the 256 MB
+Infinity Cache and the L2s start cold, as the reference's timing does with
+its L2 flush. Timed: exactly K steps between synchronizations, each bracketed
+by HIP events on the replay stream; ms_per_step is their median and value is
+useful TFLOP/s = 2*2*T*k*D*F / step time (padding FLOPs not counted).
+
+Also reported (same JSON line): eager-mode layer time, per-stage times from
+events at the layer's stage marks (each of SDD and DSD is exactly one kernel,
+so its stage time is that kernel's duration on its stream), the roofline of
+the dominant kernel, and the CPU baseline: the oracle's fp32 loop-over-experts
+layer on this host's cores, timed on a bounded sample.
+
+Before timing, the layer's output is checked against a plain-torch fp32
+reference on the GPU (max |err| / max |ref| <= 2e-2); a wrong layer is not timed.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
+FLUSH_BYTES = 512 * 1024 * 1024
+REL_GATE = 2e-2
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--config", default="fine_grained", choices=["fine_grained", "mixtral", "replay_sweep"])
+    p.add_argument("--routing", default="random", choices=["random", "zipf_perm", "zipf"])
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-stages", action="store_true", help="skip the eager per-stage breakdown")
+    p.add_argument("--kernel-loop", type=int, default=0,
+                   help="after the bench, replay the graph N more times (for rocprofv3 runs)")
+    return p.parse_args()
+
+
+def fp32_reference_gpu(x, idx, gates, w1, w2) -> torch.Tensor:
+    """Loop over experts in fp32 on the GPU (exact-erf GELU): the correctness gate."""
+    out = torch.zeros(x.shape[0], x.shape[1], dtype=torch.float32, device=x.device)
+    for e in range(w1.shape[0]):
+        token, slot = torch.nonzero(idx == e, as_tuple=True)
+        if token.numel():
+            h = x[token].float() @ w1[e].float()
+            h = 0.5 * h * (1.0 + torch.erf(h * 0.7071067811865476))
+            out.index_add_(0, token, (h @ w2[e].float()) * gates[token, slot, None].float())
+    return out
+
+
+def algorithmic_bytes(shape, active_experts: int) -> dict[str, int]:
+    """Bytes each stage must move at least: inputs read once, outputs written once, no padding."""
+    t, d, f, k = shape.num_tokens, shape.d_model, shape.ffn_dim, shape.top_k
+    n = t * k
+    return {
+        "sdd": t * d * 2 + active_experts * d * f * 2 + n * f * 2,
+        "dsd": n * f * 2 + active_experts * f * d * 2 + n * d * 2,
+        "combine": n * d * 2 + n * (2 + 4) + t * d * 2,
+    }
+
+
+def cpu_baseline(shape, routing: str, seed: int) -> dict:
+    """The oracle's fp32 layer on the host cores, on a bounded sample of the workload.
+
+    Sample: the first 8 of the E experts' work (every token routed to them),
+    i.e. about 8/E of the layer, scaled to useful TFLOP/s by its own FLOPs.
+    """
+    from oracle.moe_ref import moe_reference  # CPU baseline leg only
+    from sparsebench_amd.workloads import make_layer
+
+    threads = torch.get_num_threads()
+    x, idx, gates, w1, w2 = make_layer(shape, routing, seed, device="cpu", dtype=torch.float32)
+    sample_experts = min(8, shape.num_experts)
+    keep = (idx < sample_experts)
+    copies = int(keep.sum())
+    # The layer restricted to the sample: copies to other experts get an id the
+    # expert loop never visits, so they cost nothing.
+    idx_s = torch.where(keep, idx, torch.full_like(idx, sample_experts))
+    w1_s, w2_s = w1[:sample_experts].contiguous(), w2[:sample_experts].contiguous()
+    moe_reference(x[:64], idx_s[:64], gates[:64], w1_s, w2_s)  # warm up
+    times = []
+    budget_s = 20.0
+    start_all = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start_all < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        moe_reference(x, idx_s, gates, w1_s, w2_s)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - start_all > budget_s:
+            break
+    flops = 2 * 2 * copies * shape.d_model * shape.ffn_dim
+    sec = statistics.median(times)
+    return {
+        "value": round(flops / sec / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle fp32 loop-over-experts layer (oracle/moe_ref.py) on {shape.name}, {routing} routing, "
+                   f"experts 0..{sample_experts - 1} only ({copies} of {shape.num_tokens * shape.top_k} copies), "
+                   f"median of {len(times)} runs, {sec * 1e3:.1f} ms each, torch CPU with {threads} threads"),
+        "ms_per_sample": round(sec * 1e3, 3),
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build's path is single-GPU (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X)", file=sys.stderr)
+        return 2
+
+    from sparsebench_amd.moe import moe_forward
+    from sparsebench_amd.workloads import SHAPES, make_layer
+
+    shape = SHAPES[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    x, idx, gates, w1, w2 = make_layer(shape, args.routing, args.seed, device=dev)
+    gates = gates.to(torch.bfloat16)
+    active = int(torch.unique(idx).numel())
+    print(f"[bench] {shape} routing={args.routing} active_experts={active}", flush=True)
+
+    # ---- correctness gate ----
+    out = moe_forward(x, idx, gates, w1, w2)
+    ref = fp32_reference_gpu(x, idx, gates, w1, w2)
+    rel = float((out.float() - ref).abs().max() / ref.abs().max())
+    print(f"[bench] correctness: max rel err {rel:.3e} (gate {REL_GATE})", flush=True)
+    if not rel <= REL_GATE:
+        print(json.dumps({"error": f"wrong answer: max rel err {rel}"}))
+        return 1
+    del ref
+
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+
+    # ---- capture the layer once ----
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            moe_forward(x, idx, gates, w1, w2)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        g_out = moe_forward(x, idx, gates, w1, w2)
+    torch.cuda.synchronize()
+
+    def timed_replays(n: int) -> list[float]:
+        samples = []
+        with torch.cuda.stream(stream):
+            for _ in range(n):
+                flush.zero_()
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record(stream)
+                graph.replay()
+                e.record(stream)
+                samples.append((s, e))
+        torch.cuda.synchronize()
+        return [s.elapsed_time(e) for s, e in samples]
+
+    timed_replays(args.warmup)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    samples = timed_replays(args.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = statistics.median(samples)
+    assert torch.equal(g_out, moe_forward(x, idx, gates, w1, w2)), "graph replay differs from eager"
+    print(f"[bench] graph replay: median {ms:.4f} ms over {args.steps} steps (min {min(samples):.4f})", flush=True)
+
+    # ---- eager layer and per-stage times ----
+    stages: dict[str, float] = {}
+    eager_ms = None
+    if not args.no_stages:
+        per_stage: dict[str, list[float]] = {}
+        totals = []
+        for it in range(args.warmup + args.steps):
+            flush.zero_()
+            events: list[tuple[str, torch.cuda.Event]] = []
+
+            def mark(stage: str) -> None:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record()
+                events.append((stage, ev))
+
+            start = torch.cuda.Event(enable_timing=True)
+            start.record()
+            moe_forward(x, idx, gates, w1, w2, mark=mark)
+            torch.cuda.synchronize()
+            if it < args.warmup:
+                continue
+            prev = start
+            for stage, ev in events:
+                per_stage.setdefault(stage, []).append(prev.elapsed_time(ev))
+                prev = ev
+            totals.append(start.elapsed_time(events[-1][1]))
+        stages = {s: round(statistics.median(v), 4) for s, v in per_stage.items()}
+        eager_ms = round(statistics.median(totals), 4)
+        print(f"[bench] eager: {eager_ms} ms, stages {stages}", flush=True)
+
+    # ---- roofline of the dominant kernel (SDD or DSD, one kernel each) ----
+    nbytes = algorithmic_bytes(shape, active)
+    roofline = None
+    if stages:
+        sdd_ms, dsd_ms = stages["SDD + GELU (fused)"], stages["DSD"]
+        name, kms = ("sdd", sdd_ms) if sdd_ms >= dsd_ms else ("dsd", dsd_ms)
+        flops = shape.useful_flops // 2
+        ai = flops / nbytes[name]
+        hbm_bound = ai < MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+        if hbm_bound:
+            achieved = nbytes[name] / (kms * 1e-3) / 1e9
+            roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": f"{name}_kernel",
+                        "algorithmic_bytes": nbytes[name], "kernel_ms": kms,
+                        "useful_tflops": round(flops / (kms * 1e-3) / 1e12, 2)}
+        else:
+            achieved = flops / (kms * 1e-3) / 1e12
+            roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                        "kernel": f"{name}_kernel", "useful_flops": flops, "kernel_ms": kms}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] CPU baseline ...", flush=True)
+        cpu = cpu_baseline(shape, args.routing, args.seed)
+        print(f"[bench] CPU baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads", flush=True)
+
+    if args.kernel_loop:
+        with torch.cuda.stream(stream):
+            for _ in range(args.kernel_loop):
+                graph.replay()
+        torch.cuda.synchronize()
+
+    tflops = shape.useful_flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "MoE fwd layer ms + useful TFLOP/s, D1024 F4096 E64, 4096 tok top-2 bf16",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded x, routing, random-init weights)",
+        "config": {"workload": f"{shape.name} MoE forward layer", "tokens": shape.num_tokens,
+                   "d_model": shape.d_model, "ffn_dim": shape.ffn_dim, "experts": shape.num_experts,
+                   "top_k": shape.top_k, "routing": args.routing, "block_size": 128,
+                   "timing": "hipGraph replay, 512 MiB cache flush between steps, median"},
+        "layer_ms_eager": eager_ms,
+        "stages_ms": stages,
+        "wall_s_timed_steps": round(wall, 4),
+        "max_rel_err": rel,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,101 @@
+/* sparsebench_hip.h: C ABI of the MI355X (gfx950) MoE forward path.
+ *
+ * One shared library, libsparsebench_hip.so, built by hipcc for gfx950 only.
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as void*, so a binder needs no HIP headers), enqueues work on that
+ * stream and returns at once: no allocation, no host sync, no hipMalloc, so
+ * every call may be recorded into a HIP graph. Buffers are owned by the
+ * caller. Return value: SB_OK, or an SB_ERR_* code with a message readable
+ * through sb_last_error() on the calling thread.
+ *
+ * Each entry point names the reference interface it replaces, in
+ * saransh-debugs/SparseBench (paths relative to that repository).
+ */
+#ifndef SPARSEBENCH_HIP_H_
+#define SPARSEBENCH_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SB_OK 0
+#define SB_ERR_INVALID 1 /* bad argument: shape, size, alignment, range */
+#define SB_ERR_HIP 2     /* a HIP runtime call or kernel launch failed */
+
+/* Element type codes for sb_combine's gate weights. */
+#define SB_DTYPE_BF16 0
+#define SB_DTYPE_F16 1
+#define SB_DTYPE_F32 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* sb_last_error(void);
+
+/* Library version, for a binder to check it loaded the right file. */
+int32_t sb_version(void);
+
+/* Replaces arch_probe (csrc/smoke.cu:23-38, csrc/ops.hpp:11).
+ * Writes the architecture number of the code that ran (950 on gfx950)
+ * into out[0..n). n must be positive. */
+int sb_arch_probe(int32_t* out, int64_t n, void* stream);
+
+/* Worst-case sizes of the routing outputs for n = T*k copies
+ * (csrc/routing.cu:306-311). Host-only arithmetic; returns SB_ERR_INVALID
+ * when the problem does not fit int32 indexing. */
+int sb_routing_sizes(int64_t num_copies, int32_t num_experts, int32_t ffn_dim, int32_t block_size,
+                     int64_t* max_row_blocks, int64_t* max_rows, int64_t* workspace_elems);
+
+/* Replaces build_topology_cuda (csrc/routing.cu:291-375, csrc/ops.hpp:20-21).
+ * expert_idx: [T, k] int32 (idx_is_i64 = 0) or int64 (idx_is_i64 = 1).
+ * Writes, for the worst-case sizes given by sb_routing_sizes:
+ *   tokens_per_expert[E], padded_offsets[E+1], row_token[max_rows],
+ *   copy_row[T*k], row_block_expert[max_row_blocks],
+ *   row_offsets[max_row_blocks+1], col_indices[max_row_blocks*ffn_blocks],
+ *   error[1] (1 if any expert id was outside [0, E), else 0).
+ * workspace: workspace_elems int32 of scratch, owned by the caller.
+ * valid_tokens: NULL for the reference behaviour; otherwise a device int32
+ * holding T' <= T, and copies of tokens >= T' are neither counted nor
+ * flagged (copy_row = -1): a graph captured at T can replay at T' <= T.
+ * Outputs are bit-identical to sparsebench/topology.py:build_topology on the
+ * live part, with the past-the-end conventions of routing.cu:256-287. */
+int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, int32_t k, int32_t num_experts,
+               int32_t ffn_dim, int32_t block_size, const int32_t* valid_tokens, int32_t* workspace,
+               int32_t* tokens_per_expert, int32_t* padded_offsets, int32_t* row_token, int32_t* copy_row,
+               int32_t* row_block_expert, int32_t* row_offsets, int32_t* col_indices, int32_t* error, void* stream);
+
+/* Replaces sdd_cuda (csrc/sdd.cu:123-170, csrc/ops.hpp:34-36).
+ * out[num_row_blocks*F/128, 128, 128] bf16 = (gelu)(x[row_token] @ w1[expert])
+ * on the layout's blocks. x [T, D] bf16, w1 [E, D, F] bf16, 16-byte aligned;
+ * D % 64 == 0, F % 256 == 0; row_token has num_row_blocks*128 entries.
+ * Rows with row_token < 0 are zero (no read of x); row blocks with
+ * row_offsets[r] == row_offsets[r+1] are skipped and their blocks left unwritten. */
+int sb_sdd(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+           const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
+           int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, void* stream);
+
+/* Replaces dsd_cuda's kernels (csrc/dsd.cpp:27-80, csrc/dsd_v5.cu:106-123,
+ * csrc/ops.hpp:27-28).
+ * out[num_row_blocks*bs, D] bf16 = BSR(blocks, row_offsets, col_indices) @ w.
+ * blocks [nnz, bs, bs] bf16, w [w_rows, D] bf16, bs in {64, 128}, D % 128 == 0.
+ * zero_dead_rows = 1 writes zeros for row blocks with no blocks (the contract
+ * of versions 1-3); 0 leaves them unwritten (versions 4, 41, 5). */
+int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices, void* out,
+           int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t block_size, int64_t d_model,
+           int32_t zero_dead_rows, void* stream);
+
+/* Replaces the combine step of moe_forward (sparsebench/moe.py:51-54).
+ * out[t, :] = bf16( sum_j fp32(y[copy_row[t*k+j], :]) * fp32(gates[t*k+j]) ),
+ * j in [0, k), fp32 accumulation. Copies with copy_row < 0 add nothing.
+ * y [y_rows, D] bf16, out [T, D] bf16, gates [T, k] of gate_dtype, D % 8 == 0.
+ * valid_tokens: NULL, or a device int32 T' <= T: rows t >= T' are not written. */
+int sb_combine(const void* y, const int32_t* copy_row, const void* gates, int32_t gate_dtype, void* out,
+               int64_t num_tokens, int32_t k, int64_t d_model, int64_t y_rows, const int32_t* valid_tokens,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSEBENCH_HIP_H_ */

@@ -1,0 +1,266 @@
+"""The operator surface of the reference's pybind11 module `sparsebench._C`
+(csrc/bindings.cpp:5-16, csrc/ops.hpp:11-36), over the gfx950 C ABI.
+
+Same four functions, same keyword names, same outputs, and the same
+RuntimeError messages for bad arguments (the checks of csrc/routing.cu:198-224,
+csrc/sdd.cu:126-153, csrc/dsd.cpp:29-61, csrc/dsd_v5.cu:108-110,
+csrc/smoke.cu:24), in the same order. Outputs come from torch's caching
+allocator on the input's device and all work is enqueued on torch's current
+stream, so nothing here syncs and every call can be captured in a graph.
+
+combine_cuda is this build's addition: the combine step of moe_forward as one
+kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from sparsebench_amd._lib import check, lib, stream_of
+
+_I32_MAX = 2**31 - 1
+_MAX_EXPERTS = 1024
+_DSD_TILE_N = 128
+# dsd version code -> dead row blocks written as zeros (versions 1-3) or left unwritten (4 on)
+_DSD_VERSIONS = {1: True, 2: True, 21: True, 3: True, 31: True, 4: False, 41: False, 5: False}
+_GATE_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _fail(msg: str) -> None:
+    raise RuntimeError(msg)
+
+
+def _shape(t: torch.Tensor) -> str:
+    return "[" + ", ".join(str(s) for s in t.shape) + "]"
+
+
+def _check_index(t: torch.Tensor, name: str) -> None:
+    if not (t.is_cuda and t.dtype == torch.int32 and t.dim() == 1 and t.is_contiguous()):
+        _fail(f"{name} must be a contiguous 1-D int32 CUDA tensor")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def arch_probe(n: int) -> torch.Tensor:
+    """int32[n] filled with the architecture number of the code that ran (950 on gfx950)."""
+    if n <= 0:
+        _fail(f"arch_probe: n must be positive, got {n}")
+    out = torch.empty(n, dtype=torch.int32, device="cuda")
+    check(lib().sb_arch_probe(out.data_ptr(), n, stream_of(out.device)))
+    return out
+
+
+def routing_sizes(num_copies: int, num_experts: int, ffn_dim: int, block_size: int) -> tuple[int, int, int]:
+    """(max_row_blocks, max_rows, workspace int32 elements) for n = T*k copies."""
+    rb, rows, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    check(lib().sb_routing_sizes(num_copies, num_experts, ffn_dim, block_size,
+                                 ctypes.byref(rb), ctypes.byref(rows), ctypes.byref(ws)))
+    return rb.value, rows.value, ws.value
+
+
+def build_topology_cuda(
+    expert_idx: torch.Tensor,
+    num_experts: int,
+    ffn_dim: int,
+    block_size: int,
+    valid_tokens: torch.Tensor | None = None,
+) -> list[torch.Tensor]:
+    """Routing -> block-sparse layout on the GPU, no host sync.
+
+    Returns, in order: tokens_per_expert [E], padded_offsets [E+1],
+    row_token [max_rows], copy_row [T*k], row_block_expert [max_row_blocks],
+    row_offsets [max_row_blocks+1], col_indices [max_row_blocks*ffn_blocks],
+    error [1] (all int32; csrc/ops.hpp:13-21).
+
+    valid_tokens (this build's extension, default None = reference behaviour):
+    an int32 CUDA scalar T' <= T; copies of tokens >= T' are ignored.
+    """
+    if not expert_idx.is_cuda:
+        _fail("expert_idx must be a CUDA tensor")
+    if expert_idx.dim() != 2 or expert_idx.shape[0] == 0 or expert_idx.shape[1] == 0:
+        _fail(f"expert_idx must be [T, k] with T, k > 0, got {_shape(expert_idx)}")
+    if expert_idx.dtype not in (torch.int32, torch.int64):
+        _fail(f"expert_idx must be int32 or int64, got {expert_idx.dtype}")
+    if not expert_idx.is_contiguous():
+        _fail("expert_idx must be contiguous")
+    if not 0 < num_experts <= _MAX_EXPERTS:
+        _fail(f"num_experts must be in [1, {_MAX_EXPERTS}], got {num_experts}")
+    if not 0 < block_size <= _I32_MAX:
+        _fail("block_size must be in [1, 2^31)")
+    if ffn_dim <= 0 or ffn_dim % block_size != 0:
+        _fail(f"ffn_dim ({ffn_dim}) must be a positive multiple of block_size ({block_size})")
+    num_tokens, k = expert_idx.shape
+    n = num_tokens * k
+    # Worst case: every expert wastes block_size - 1 rows (csrc/routing.cu:306-318).
+    max_row_blocks = (n + num_experts * (block_size - 1)) // block_size
+    max_rows = max_row_blocks * block_size
+    ffn_blocks = ffn_dim // block_size
+    if max_rows > _I32_MAX // ffn_dim or max_row_blocks * ffn_blocks >= _I32_MAX or n > _I32_MAX:
+        _fail("problem too large for int32 indexing")
+    if valid_tokens is not None:
+        if not (valid_tokens.is_cuda and valid_tokens.dtype == torch.int32 and valid_tokens.numel() == 1):
+            _fail("valid_tokens must be a one-element int32 CUDA tensor")
+
+    dev = expert_idx.device
+    opts = {"dtype": torch.int32, "device": dev}
+    num_chunks = (n + 1023) // 1024
+    workspace = torch.empty(num_chunks * (num_experts + 1), **opts)
+    tokens_per_expert = torch.empty(num_experts, **opts)
+    padded_offsets = torch.empty(num_experts + 1, **opts)
+    row_token = torch.empty(max_rows, **opts)
+    copy_row = torch.empty(n, **opts)
+    row_block_expert = torch.empty(max_row_blocks, **opts)
+    row_offsets = torch.empty(max_row_blocks + 1, **opts)
+    col_indices = torch.empty(max_row_blocks * ffn_blocks, **opts)
+    error = torch.empty(1, **opts)
+    check(lib().sb_routing(
+        expert_idx.data_ptr(), 1 if expert_idx.dtype == torch.int64 else 0, num_tokens, k, num_experts, ffn_dim,
+        block_size, _ptr(valid_tokens), workspace.data_ptr(), tokens_per_expert.data_ptr(),
+        padded_offsets.data_ptr(), row_token.data_ptr(), copy_row.data_ptr(), row_block_expert.data_ptr(),
+        row_offsets.data_ptr(), col_indices.data_ptr(), error.data_ptr(), stream_of(dev),
+    ))
+    return [tokens_per_expert, padded_offsets, row_token, copy_row, row_block_expert, row_offsets, col_indices, error]
+
+
+def sdd_cuda(
+    x: torch.Tensor,
+    w1: torch.Tensor,
+    row_token: torch.Tensor,
+    row_block_expert: torch.Tensor,
+    row_offsets: torch.Tensor,
+    num_nnz: int,
+    apply_gelu: bool,
+) -> torch.Tensor:
+    """H blocks [num_nnz, 128, 128] bf16 = (gelu)(x[row_token] @ w1[expert]) on the layout's blocks."""
+    if not (x.is_cuda and w1.is_cuda and x.device == w1.device):
+        _fail("x and w1 must be on the same GPU")
+    if x.dtype != torch.bfloat16 or w1.dtype != torch.bfloat16:
+        _fail("x and w1 must be bfloat16")
+    if not (x.is_contiguous() and w1.is_contiguous()):
+        _fail("x and w1 must be contiguous")
+    if not (x.dim() == 2 and w1.dim() == 3 and w1.shape[1] == x.shape[1]):
+        _fail(f"x must be [T, D] and w1 [E, D, F], got {_shape(x)} and {_shape(w1)}")
+    _check_index(row_token, "row_token")
+    _check_index(row_block_expert, "row_block_expert")
+    _check_index(row_offsets, "row_offsets")
+    if x.data_ptr() % 16 or w1.data_ptr() % 16:
+        _fail("x and w1 must be 16-byte aligned")
+    d_model, ffn_dim = x.shape[1], w1.shape[2]
+    num_row_blocks = row_offsets.numel() - 1
+    if d_model <= 0 or d_model % 64:
+        _fail(f"sdd needs D ({d_model}) to be a multiple of 64")
+    if ffn_dim <= 0 or ffn_dim % 256:
+        _fail(f"sdd needs F ({ffn_dim}) to be a multiple of 256")
+    if row_token.numel() != num_row_blocks * 128:
+        _fail(f"sdd needs block size 128: row_token has {row_token.numel()} rows for {num_row_blocks} row blocks")
+    if row_block_expert.numel() != num_row_blocks:
+        _fail("row_block_expert must have one entry per row block")
+    if num_nnz != num_row_blocks * (ffn_dim // 128):
+        _fail(f"expected {num_row_blocks * (ffn_dim // 128)} blocks (row blocks x F/128), got {num_nnz}")
+    if num_row_blocks * (ffn_dim // 256) > _I32_MAX or ffn_dim * d_model > _I32_MAX:
+        _fail("problem too large")
+    out = torch.empty(num_nnz, 128, 128, dtype=w1.dtype, device=w1.device)
+    if num_row_blocks <= 0:
+        return out
+    check(lib().sb_sdd(
+        x.data_ptr(), w1.data_ptr(), row_token.data_ptr(), row_block_expert.data_ptr(), row_offsets.data_ptr(),
+        out.data_ptr(), x.shape[0], d_model, ffn_dim, w1.shape[0], num_row_blocks, 1 if apply_gelu else 0,
+        stream_of(x.device),
+    ))
+    return out
+
+
+def dsd_cuda(
+    blocks: torch.Tensor, w: torch.Tensor, row_offsets: torch.Tensor, col_indices: torch.Tensor, version: int
+) -> torch.Tensor:
+    """out [(len(row_offsets)-1)*bs, D] bf16 = BSR(blocks, row_offsets, col_indices) @ w.
+
+    Every version code of the reference is accepted and gives the same
+    results; codes 1, 2, 21, 3, 31 write dead row blocks as zeros, codes 4,
+    41, 5 leave them unwritten, and 5 needs block size 128 and D % 256 == 0.
+    """
+    if not (blocks.is_cuda and w.is_cuda):
+        _fail("blocks and w must be CUDA tensors")
+    if not (blocks.device == w.device and row_offsets.device == w.device and col_indices.device == w.device):
+        _fail("all inputs must be on the same GPU")
+    if blocks.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        _fail("blocks and w must be bfloat16")
+    if not (blocks.is_contiguous() and w.is_contiguous()):
+        _fail("blocks and w must be contiguous")
+    if not (blocks.dim() == 3 and blocks.shape[1] == blocks.shape[2]):
+        _fail(f"blocks must be [nnz, bs, bs], got {_shape(blocks)}")
+    if w.dim() != 2:
+        _fail(f"w must be [E*F, D], got {_shape(w)}")
+    _check_index(row_offsets, "row_offsets")
+    _check_index(col_indices, "col_indices")
+    bs, d_model = blocks.shape[1], w.shape[1]
+    num_row_blocks = row_offsets.numel() - 1
+    if bs not in (64, 128):
+        _fail(f"block size must be 64 or 128, got {bs}")
+    if d_model <= 0 or d_model % _DSD_TILE_N:
+        _fail(f"D ({d_model}) must be a positive multiple of {_DSD_TILE_N}")
+    if d_model // _DSD_TILE_N > 65535:
+        _fail("D too large for grid y")
+    if w.shape[0] % bs:
+        _fail(f"w rows ({w.shape[0]}) must be a multiple of the block size ({bs})")
+    if num_row_blocks < 0:
+        _fail("row_offsets must have at least one entry")
+    if blocks.shape[0] != col_indices.numel():
+        _fail(f"blocks has {blocks.shape[0]} blocks but col_indices has {col_indices.numel()}")
+    if num_row_blocks * bs > _I32_MAX:
+        _fail("too many row blocks")
+    if num_row_blocks * (d_model // _DSD_TILE_N) > _I32_MAX:
+        _fail("too many tiles for a 1-D grid")
+    if blocks.data_ptr() % 16:
+        _fail("blocks must be 16-byte aligned")
+    if w.data_ptr() % 16:
+        _fail("w must be 16-byte aligned")
+    out = torch.empty(num_row_blocks * bs, d_model, dtype=w.dtype, device=w.device)
+    if num_row_blocks == 0:
+        return out
+    if version not in _DSD_VERSIONS:
+        _fail(f"unknown dsd version {version}")
+    if version == 5 and (bs != 128 or d_model % 256):
+        _fail(f"dsd v5 needs block size 128 and D a multiple of 256, got block size {bs}, D {d_model}")
+    check(lib().sb_dsd(
+        blocks.data_ptr(), w.data_ptr(), row_offsets.data_ptr(), col_indices.data_ptr(), out.data_ptr(),
+        blocks.shape[0], w.shape[0], num_row_blocks, bs, d_model, 1 if _DSD_VERSIONS[version] else 0,
+        stream_of(w.device),
+    ))
+    return out
+
+
+def combine_cuda(
+    y: torch.Tensor,
+    copy_row: torch.Tensor,
+    expert_weight: torch.Tensor,
+    valid_tokens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """out [T, D] bf16: each token's k rows of y, gate-weighted, summed in fp32.
+
+    y [rows, D] bf16, copy_row [T*k] int32 (row of copy t*k+j, -1 = skipped),
+    expert_weight [T, k] bf16/fp16/fp32. Rows t >= valid_tokens (if given) are
+    left unwritten.
+    """
+    if not (y.is_cuda and copy_row.is_cuda and expert_weight.is_cuda):
+        _fail("y, copy_row and expert_weight must be CUDA tensors")
+    if y.dtype != torch.bfloat16 or y.dim() != 2 or not y.is_contiguous():
+        _fail(f"y must be a contiguous [rows, D] bfloat16 tensor, got {_shape(y)} {y.dtype}")
+    _check_index(copy_row, "copy_row")
+    if expert_weight.dim() != 2 or expert_weight.numel() != copy_row.numel():
+        _fail(f"expert_weight must be [T, k] with T*k == len(copy_row), got {_shape(expert_weight)}")
+    gates = expert_weight if expert_weight.dtype in _GATE_DTYPES else expert_weight.float()
+    gates = gates.contiguous()
+    num_tokens, k = expert_weight.shape
+    out = torch.empty(num_tokens, y.shape[1], dtype=y.dtype, device=y.device)
+    if num_tokens == 0:
+        return out
+    check(lib().sb_combine(
+        y.data_ptr(), copy_row.data_ptr(), gates.data_ptr(), _GATE_DTYPES[gates.dtype], out.data_ptr(),
+        num_tokens, k, y.shape[1], y.shape[0], _ptr(valid_tokens), stream_of(y.device),
+    ))
+    return out

@@ -1,0 +1,166 @@
+// DSD: block-sparse (BSR) x dense on gfx950 (the operation of the reference's
+// csrc/dsd_v1.cu .. dsd_v5.cu, one kernel here for every version code).
+//
+//   out[r*bs + i, n] = sum_{p in [row_offsets[r], row_offsets[r+1])}
+//                      sum_{kk < bs} blocks[p][i][kk] * w[col_indices[p]*bs + kk, n]
+//
+// One workgroup computes bs x BN outputs of one row block, walking its
+// blocks in K steps of 64 (two per block at bs = 128, one at bs = 64) on the
+// shared MFMA tile loop. Dead row blocks are skipped, or written as zeros
+// when zero_dead_rows is set (the contract of the reference's versions 1-3).
+// Tiles are row block first and spread over the XCDs in contiguous ranges,
+// so a row block's column slices and an expert's row blocks share an L2.
+
+#include <type_traits>
+
+#include "gemm_tile.hpp"
+
+namespace sb {
+namespace {
+
+template <class Cfg>
+struct DsdLoader {
+  using ML = Mainloop<Cfg>;
+  using BRow = typename Cfg::BRow;
+  static constexpr int kStepsPerBlock = Cfg::BM / Cfg::BK;
+  const uint16_t* blocks;
+  const uint16_t* w_cols;  // w + n0
+  const int32_t* col_indices;
+  int64_t d_model, w_rows;
+  int32_t begin;
+
+  // Block p and the K offset inside it of K step t.
+  __device__ __forceinline__ void step(int t, int32_t* p, int* kin) const {
+    *p = begin + t / kStepsPerBlock;
+    *kin = (t % kStepsPerBlock) * Cfg::BK;
+  }
+
+  __device__ __forceinline__ void load_a(int t, const typename ML::LoadPos& pos, u32x4_t (&a)[Cfg::kAChunks]) const {
+    int32_t p;
+    int kin;
+    step(t, &p, &kin);
+    const uint16_t* blk = blocks + static_cast<int64_t>(p) * Cfg::BM * Cfg::BM + kin + pos.a_chunk * 8;
+#pragma unroll
+    for (int j = 0; j < Cfg::kAChunks; ++j)
+      a[j] = *reinterpret_cast<const u32x4_t*>(blk + static_cast<int64_t>(pos.a_row[j]) * Cfg::BM);
+  }
+
+  __device__ __forceinline__ void load_b(int t, const typename ML::LoadPos& pos, BRow (&b)[8]) const {
+    int32_t p;
+    int kin;
+    step(t, &p, &kin);
+    const int64_t row0 = static_cast<int64_t>(col_indices[p]) * Cfg::BM;
+    if (row0 < 0 || row0 + Cfg::BM > w_rows) {  // not a block of w: contributes nothing
+#pragma unroll
+      for (int r = 0; r < 8; ++r) b[r] = BRow{};
+      return;
+    }
+    const uint16_t* src = w_cols + (row0 + kin + pos.b_kgroup * 8) * d_model + pos.b_col;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) b[r] = *reinterpret_cast<const BRow*>(src + r * d_model);
+  }
+};
+
+template <int BM, int BN>
+__global__ void __launch_bounds__(256)
+    dsd_kernel(const uint16_t* __restrict__ blocks, const uint16_t* __restrict__ w,
+               const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ col_indices,
+               uint16_t* __restrict__ out, int64_t nnz, int64_t w_rows, int32_t num_row_blocks, int32_t d_model,
+               int32_t num_slices, int32_t zero_dead_rows) {
+  using Cfg = TileCfg<BM, BN>;
+  using ML = Mainloop<Cfg>;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::kLdsElems];
+
+  const int live = (zero_dead_rows ? num_row_blocks : live_row_blocks(row_offsets, num_row_blocks)) * num_slices;
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live);
+  const int rb = tile / num_slices;
+  const int n0 = (tile % num_slices) * BN;
+  int32_t begin = row_offsets[rb];
+  int32_t end = row_offsets[rb + 1];
+  if (begin < 0 || end > nnz || end < begin) begin = end = 0;  // not a BSR row: treat as empty
+
+  uint16_t* out_tile = out + static_cast<int64_t>(rb) * BM * d_model + n0;
+  if (begin == end) {
+    if (!zero_dead_rows) return;
+    // BM x BN zeros, 16 bytes per store.
+    constexpr int kChunksPerRow = BN / 8;
+    for (int q = threadIdx.x; q < BM * kChunksPerRow; q += Cfg::kThreads) {
+      const int r = q / kChunksPerRow, c = q % kChunksPerRow;
+      *reinterpret_cast<u32x4_t*>(out_tile + static_cast<int64_t>(r) * d_model + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+
+  DsdLoader<Cfg> ld;
+  ld.blocks = blocks;
+  ld.w_cols = w + n0;
+  ld.col_indices = col_indices;
+  ld.d_model = d_model;
+  ld.w_rows = w_rows;
+  ld.begin = begin;
+
+  typename ML::Acc acc;
+  ML::run(lds, ld, (end - begin) * DsdLoader<Cfg>::kStepsPerBlock, acc);
+
+#pragma unroll
+  for (int j = 0; j < Cfg::TN; ++j) {
+    uint16_t* col = out_tile + ML::acc_col(j);
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) col[static_cast<int64_t>(ML::acc_row(i, v)) * d_model] = f32_to_bf16(acc[i][j][v]);
+  }
+}
+
+template <int BM, int BN>
+int launch_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices, void* out,
+               int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t d_model, int32_t zero_dead_rows,
+               hipStream_t stream) {
+  const int32_t num_slices = static_cast<int32_t>(d_model / BN);
+  const int64_t tiles = num_row_blocks * num_slices;
+  dsd_kernel<BM, BN><<<static_cast<uint32_t>(tiles), 256, 0, stream>>>(
+      static_cast<const uint16_t*>(blocks), static_cast<const uint16_t*>(w), row_offsets, col_indices,
+      static_cast<uint16_t*>(out), nnz, w_rows, static_cast<int32_t>(num_row_blocks), static_cast<int32_t>(d_model),
+      num_slices, zero_dead_rows);
+  return check_launch("dsd");
+}
+
+}  // namespace
+}  // namespace sb
+
+using namespace sb;
+
+extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices,
+                      void* out, int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t block_size,
+                      int64_t d_model, int32_t zero_dead_rows, void* stream) {
+  constexpr int64_t kI32Max = 2147483647;
+  if (block_size != 64 && block_size != 128)
+    return fail(SB_ERR_INVALID, "block size must be 64 or 128, got %lld", static_cast<long long>(block_size));
+  if (d_model <= 0 || d_model % 128 != 0)
+    return fail(SB_ERR_INVALID, "D (%lld) must be a positive multiple of 128", static_cast<long long>(d_model));
+  if (num_row_blocks < 0) return fail(SB_ERR_INVALID, "row_offsets must have at least one entry");
+  if (w_rows < 0 || w_rows % block_size != 0)
+    return fail(SB_ERR_INVALID, "w rows (%lld) must be a multiple of the block size (%lld)",
+                static_cast<long long>(w_rows), static_cast<long long>(block_size));
+  if (nnz < 0) return fail(SB_ERR_INVALID, "blocks must be [nnz, bs, bs]");
+  if (num_row_blocks * block_size > kI32Max) return fail(SB_ERR_INVALID, "too many row blocks");
+  if (num_row_blocks * (d_model / 128) > kI32Max) return fail(SB_ERR_INVALID, "too many tiles for a 1-D grid");
+  if (num_row_blocks == 0) return clear_ok();
+  if (!blocks || !w || !row_offsets || !col_indices || !out) return fail(SB_ERR_INVALID, "dsd: null buffer");
+  if (!aligned16(blocks) || !aligned16(w) || !aligned16(out))
+    return fail(SB_ERR_INVALID, "blocks and w must be 16-byte aligned");
+  const hipStream_t s = as_stream(stream);
+  // 256-column tiles halve the re-reads of each H block; 128-column tiles
+  // when D is not a multiple of 256 or there are too few tiles to fill the GPU.
+  const bool wide = d_model % 256 == 0 && num_row_blocks * (d_model / 256) >= 4 * 256;
+  if (block_size == 128) {
+    return wide ? launch_dsd<128, 256>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks,
+                                       d_model, zero_dead_rows, s)
+                : launch_dsd<128, 128>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks,
+                                       d_model, zero_dead_rows, s);
+  }
+  return wide ? launch_dsd<64, 256>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
+                                    zero_dead_rows, s)
+              : launch_dsd<64, 128>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
+                                    zero_dead_rows, s);
+}

@@ -1,0 +1,192 @@
+// The bf16 MFMA tile loop shared by SDD and DSD on gfx950.
+//
+// One workgroup of 256 lanes (4 wave64s, 2 x 2) computes a BM x BN fp32 tile
+//     acc += A[BM, K] @ B[K, BN]
+// in K steps of 64 with v_mfma_f32_32x32x16_bf16. Each wave owns a
+// (BM/2) x (BN/2) sub-tile, i.e. TM x TN blocks of 32 x 32.
+//
+// Operands. Both GEMMs read A with K contiguous (gathered token rows of x for
+// SDD, the rows of a 128 x 128 H block for DSD) and B with N contiguous (rows
+// of W1[e] or W2). MFMA wants every lane to hold 8 consecutive K values of
+// one row (A) or one column (B), so B is transposed on its way into LDS:
+// each lane loads an 8(K) x 8(N) patch (8 row loads, coalesced along N over
+// the wave), transposes it in registers with v_perm_b32, and writes 8
+// K-contiguous 16-byte chunks. LDS then holds both tiles K-contiguous,
+// 64 K = 128 bytes = 8 chunks per row, chunk c of row r stored at
+// c ^ swz(r): consecutive rows spread over all banks for the fragment reads
+// (32 rows, one chunk) and for the B transpose writes (rows 8 apart).
+//
+// Pipeline: LDS double buffer plus one K step prefetched in registers. The
+// global loads for step t+1 are issued before the MFMAs of step t and
+// written to the other LDS buffer after them: one barrier per K step.
+//
+// The caller supplies a loader with
+//   load_a(t, u32x4 (&a)[kAChunks])   this lane's A chunks of K step t
+//   load_b(t, BRow (&b)[8])           this lane's 8 B rows of K step t
+// (zeros where there is no data) and consumes acc after gemm_mainloop.
+#pragma once
+
+#include "common.hpp"
+
+namespace sb {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+template <int BM_, int BN_>
+struct TileCfg {
+  static constexpr int BM = BM_;
+  static constexpr int BN = BN_;
+  static constexpr int BK = 64;
+  static constexpr int kThreads = 256;
+  static constexpr int WM = 2, WN = 2;                 // waves along M and N
+  static constexpr int WTM = BM / WM, WTN = BN / WN;   // wave sub-tile
+  static constexpr int TM = WTM / 32, TN = WTN / 32;   // 32 x 32 MFMA blocks per wave
+  static constexpr int kAChunks = BM * (BK / 8) / kThreads;  // 16-byte A chunks per lane per K step
+  static constexpr int kBCols = BN * BK / 8 / kThreads;      // B columns per lane (each 8 K deep)
+  static constexpr int kBGroups = BN / kBCols;               // lanes along N in the B load
+  static constexpr int kAElems = BM * BK;
+  static constexpr int kStageElems = BM * BK + BN * BK;
+  static constexpr int kLdsElems = 2 * kStageElems;
+  static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must split into 2 x 2 waves of 32 x 32 blocks");
+  static_assert(kAChunks >= 1 && BM * (BK / 8) % kThreads == 0, "A chunks must divide over the lanes");
+  static_assert(kBCols == 4 || kBCols == 8, "B patch is 8 K x 4 or 8 N");
+  static_assert(kBGroups * 8 == kThreads, "8 K groups of 8 rows cover BK");
+  using BRow = typename std::conditional<kBCols == 8, u32x4_t, u32x2_t>::type;
+};
+
+// Chunk position of logical chunk c in LDS row r.
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int lds_off(int r, int c) { return r * 64 + ((c ^ swz(r)) << 3); }
+
+// 8 rows x 8 bf16 -> 8 columns x 8 bf16 (K pairs packed low/high).
+__device__ __forceinline__ void transpose8x8(const u32x4_t (&in)[8], u32x4_t (&out)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) out[i][p] = __builtin_amdgcn_perm(in[2 * p + 1][i >> 1], in[2 * p][i >> 1], sel);
+  }
+}
+__device__ __forceinline__ void transpose8x4(const u32x2_t (&in)[8], u32x4_t (&out)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) out[i][p] = __builtin_amdgcn_perm(in[2 * p + 1][i >> 1], in[2 * p][i >> 1], sel);
+  }
+}
+
+template <class Cfg>
+struct Mainloop {
+  using BRow = typename Cfg::BRow;
+  using Acc = f32x16_t[Cfg::TM][Cfg::TN];
+
+  // This lane's place in the A and B loads (fixed for the whole loop).
+  struct LoadPos {
+    int a_row[Cfg::kAChunks];  // tile row of each A chunk
+    int a_chunk;               // K chunk (0..7), the same for all of them
+    int b_kgroup;              // B rows 8*b_kgroup .. +7
+    int b_col;                 // first of kBCols B columns
+  };
+
+  __device__ __forceinline__ static LoadPos load_pos() {
+    LoadPos p;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < Cfg::kAChunks; ++j) p.a_row[j] = (tid + j * Cfg::kThreads) >> 3;
+    p.a_chunk = tid & 7;
+    p.b_kgroup = tid / Cfg::kBGroups;
+    p.b_col = (tid % Cfg::kBGroups) * Cfg::kBCols;
+    return p;
+  }
+
+  __device__ __forceinline__ static void store_stage(uint16_t* stage, const LoadPos& p,
+                                                     const u32x4_t (&a)[Cfg::kAChunks], const BRow (&b)[8]) {
+#pragma unroll
+    for (int j = 0; j < Cfg::kAChunks; ++j)
+      *reinterpret_cast<u32x4_t*>(stage + lds_off(p.a_row[j], p.a_chunk)) = a[j];
+    uint16_t* bs = stage + Cfg::kAElems;
+    u32x4_t t[Cfg::kBCols];
+    if constexpr (Cfg::kBCols == 8) transpose8x8(b, t); else transpose8x4(b, t);
+#pragma unroll
+    for (int i = 0; i < Cfg::kBCols; ++i)
+      *reinterpret_cast<u32x4_t*>(bs + lds_off(p.b_col + i, p.b_kgroup)) = t[i];
+  }
+
+  __device__ __forceinline__ static void compute_stage(const uint16_t* stage, Acc& acc) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+    const uint16_t* as = stage;
+    const uint16_t* bs = stage + Cfg::kAElems;
+#pragma unroll
+    for (int s = 0; s < Cfg::BK / 16; ++s) {
+      const int chunk = 2 * s + (lane >> 5);
+      bf16x8_t a[Cfg::TM], b[Cfg::TN];
+#pragma unroll
+      for (int i = 0; i < Cfg::TM; ++i) {
+        const int r = wm * Cfg::WTM + i * 32 + (lane & 31);
+        a[i] = *reinterpret_cast<const bf16x8_t*>(as + lds_off(r, chunk));
+      }
+#pragma unroll
+      for (int j = 0; j < Cfg::TN; ++j) {
+        const int r = wn * Cfg::WTN + j * 32 + (lane & 31);
+        b[j] = *reinterpret_cast<const bf16x8_t*>(bs + lds_off(r, chunk));
+      }
+#pragma unroll
+      for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  template <class Loader>
+  __device__ __forceinline__ static void run(uint16_t* lds, Loader& ld, int num_steps, Acc& acc) {
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    if (num_steps <= 0) return;
+
+    const LoadPos pos = load_pos();
+    u32x4_t ra[Cfg::kAChunks];
+    BRow rb[8];
+    ld.load_a(0, pos, ra);
+    ld.load_b(0, pos, rb);
+    store_stage(lds, pos, ra, rb);
+    __syncthreads();
+
+    for (int t = 0; t < num_steps; ++t) {
+      const bool more = t + 1 < num_steps;
+      if (more) {
+        ld.load_a(t + 1, pos, ra);
+        ld.load_b(t + 1, pos, rb);
+      }
+      compute_stage(lds + (t & 1) * Cfg::kStageElems, acc);
+      if (more) store_stage(lds + ((t + 1) & 1) * Cfg::kStageElems, pos, ra, rb);
+      __syncthreads();
+    }
+  }
+
+  // Tile coordinates of accumulator value v of block (i, j) for this lane:
+  // the 32 x 32 MFMA result layout (column = lane % 32, four groups of four
+  // consecutive rows).
+  __device__ __forceinline__ static int acc_row(int i, int v) {
+    const int lane = threadIdx.x & 63;
+    const int wm = (threadIdx.x >> 6) / Cfg::WN;
+    return wm * Cfg::WTM + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+  }
+  __device__ __forceinline__ static int acc_col(int j) {
+    const int lane = threadIdx.x & 63;
+    const int wn = (threadIdx.x >> 6) % Cfg::WN;
+    return wn * Cfg::WTN + j * 32 + (lane & 31);
+  }
+};
+
+}  // namespace sb

@@ -1,0 +1,317 @@
+// Routing -> block-sparse layout on gfx950, with no host sync.
+//
+// A copy is one (token, choice) pair, c = t*k + j. Copies are sorted by
+// expert with a stable counting sort, padded per expert to a multiple of the
+// block size, and described as BSR for the two matmuls. The result is the
+// layout of sparsebench/topology.py:58-123 (reference), bit for bit, with the
+// worst-case buffer conventions of csrc/routing.cu:256-287.
+//
+// Three launches, all on the caller's stream:
+//   1. count    one workgroup per chunk of 1024 copies: per-expert counts of
+//               the chunk, plus a count of bad ids in column E.
+//   2. offsets  one workgroup: exclusive prefix of every expert's column over
+//               the chunks (in place), tokens_per_expert, padded_offsets, error.
+//   3. place    first C workgroups: each copy's row, ranked inside its wave
+//               by ballot bit-slicing (no atomics, so the order is stable);
+//               the remaining workgroups write row_offsets / col_indices /
+//               row_block_expert and mark every non-copy row -1.
+// Place's two roles touch disjoint memory and depend only on step 2.
+
+#include "common.hpp"
+
+namespace sb {
+namespace {
+
+constexpr int kChunk = 1024;             // copies per count/place workgroup, one per lane
+constexpr int kWaves = kChunk / 64;      // 16 wave64s
+constexpr int kMaxExperts = 1024;
+constexpr int kLayoutItemsPerGroup = 1024;
+
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int lane = threadIdx.x & 63;
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Mask of the wave's lanes that hold a valid copy of the same expert as this
+// lane: AND of one ballot per bit of the expert id. ceil(log2 E) ballots.
+__device__ __forceinline__ uint64_t same_expert_lanes(bool valid, int32_t e, int num_bits) {
+  uint64_t peers = __ballot(valid);
+  for (int b = 0; b < num_bits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t ones = __ballot(valid && bit);
+    peers &= bit ? ones : ~ones;
+  }
+  return peers;
+}
+
+template <typename Idx>
+__device__ __forceinline__ int32_t read_expert(const Idx* __restrict__ idx, int64_t c, int64_t n, int32_t k,
+                                               int32_t num_experts, const int32_t* __restrict__ valid_tokens,
+                                               bool* bad) {
+  *bad = false;
+  if (c >= n) return -1;
+  if (valid_tokens != nullptr && c / k >= static_cast<int64_t>(*valid_tokens)) return -1;
+  const Idx v = idx[c];
+  if (v >= 0 && v < static_cast<Idx>(num_experts)) return static_cast<int32_t>(v);
+  *bad = true;
+  return -1;
+}
+
+template <typename Idx>
+__global__ void __launch_bounds__(kChunk) route_count_kernel(const Idx* __restrict__ idx, int64_t n, int32_t k,
+                                                             int32_t num_experts, int32_t num_bits,
+                                                             const int32_t* __restrict__ valid_tokens,
+                                                             int32_t* __restrict__ counts) {
+  __shared__ int32_t hist[kMaxExperts + 1];
+  const int tid = threadIdx.x;
+  for (int e = tid; e <= num_experts; e += kChunk) hist[e] = 0;
+  __syncthreads();
+
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kChunk + tid;
+  bool bad;
+  const int32_t e = read_expert(idx, c, n, k, num_experts, valid_tokens, &bad);
+  const bool valid = e >= 0;
+  // One LDS add per distinct expert in the wave instead of one per copy:
+  // skewed routing would otherwise serialize 64 adds on one address.
+  const uint64_t peers = same_expert_lanes(valid, e, num_bits);
+  if (valid && (peers & lanes_below()) == 0) atomicAdd(&hist[e], __popcll(peers));
+  const uint64_t bad_lanes = __ballot(bad);
+  if ((tid & 63) == 0 && bad_lanes != 0) atomicAdd(&hist[num_experts], __popcll(bad_lanes));
+  __syncthreads();
+
+  int32_t* row = counts + static_cast<int64_t>(blockIdx.x) * (num_experts + 1);
+  for (int e2 = tid; e2 <= num_experts; e2 += kChunk) row[e2] = hist[e2];
+}
+
+// Inclusive scan over the 1024 lanes of one workgroup.
+__device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int64_t* wave_sums) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t below = __shfl_up(v, d, 64);
+    if (lane >= d) v += below;
+  }
+  if (lane == 63) wave_sums[wave] = v;
+  __syncthreads();
+  if (wave == 0) {
+    int64_t s = lane < kWaves ? wave_sums[lane] : 0;
+    for (int d = 1; d < kWaves; d <<= 1) {
+      const int64_t below = __shfl_up(s, d, 64);
+      if (lane >= d) s += below;
+    }
+    if (lane < kWaves) wave_sums[lane] = s;
+  }
+  __syncthreads();
+  return v + (wave > 0 ? wave_sums[wave - 1] : 0);
+}
+
+__global__ void __launch_bounds__(kChunk) route_offsets_kernel(int32_t* __restrict__ counts, int32_t num_chunks,
+                                                               int32_t num_experts, int32_t block_size,
+                                                               int32_t* __restrict__ tokens_per_expert,
+                                                               int32_t* __restrict__ padded_offsets,
+                                                               int32_t* __restrict__ error) {
+  __shared__ int64_t wave_sums[kWaves];
+  const int tid = threadIdx.x;
+  const int64_t stride = num_experts + 1;
+  int64_t padded = 0;
+  // Column col: copies of expert col (or bad ids, col == E) in each chunk,
+  // replaced in place by the copies in all earlier chunks. The loads do not
+  // depend on each other, so the unrolled walk keeps several in flight.
+  for (int col = tid; col <= num_experts; col += kChunk) {
+    int32_t total = 0;
+    int32_t b = 0;
+    for (; b + 4 <= num_chunks; b += 4) {
+      int32_t* p = counts + b * stride + col;
+      const int32_t c0 = p[0], c1 = p[stride], c2 = p[2 * stride], c3 = p[3 * stride];
+      p[0] = total;
+      p[stride] = total + c0;
+      p[2 * stride] = total + c0 + c1;
+      p[3 * stride] = total + c0 + c1 + c2;
+      total += c0 + c1 + c2 + c3;
+    }
+    for (; b < num_chunks; ++b) {
+      int32_t* p = counts + b * stride + col;
+      const int32_t c0 = *p;
+      *p = total;
+      total += c0;
+    }
+    if (col < num_experts) {
+      tokens_per_expert[col] = total;
+      padded = (static_cast<int64_t>(total) + block_size - 1) / block_size * block_size;
+    } else {
+      error[0] = total > 0 ? 1 : 0;
+    }
+  }
+  const int64_t incl = block_inclusive_scan(tid < num_experts ? padded : 0, wave_sums);
+  if (tid < num_experts) padded_offsets[tid + 1] = static_cast<int32_t>(incl);
+  if (tid == 0) padded_offsets[0] = 0;
+}
+
+template <typename Idx>
+__global__ void __launch_bounds__(kChunk)
+    route_place_kernel(const Idx* __restrict__ idx, int64_t n, int32_t k, int32_t num_experts, int32_t num_bits,
+                       const int32_t* __restrict__ valid_tokens, int32_t num_chunks,
+                       const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ tokens_per_expert,
+                       const int32_t* __restrict__ padded_offsets, int32_t block_size, int32_t ffn_blocks,
+                       int32_t max_row_blocks, int64_t max_rows, int32_t* __restrict__ copy_row,
+                       int32_t* __restrict__ row_token, int32_t* __restrict__ row_block_expert,
+                       int32_t* __restrict__ row_offsets, int32_t* __restrict__ col_indices) {
+  __shared__ int32_t lds[kWaves * kMaxExperts];  // place: per-wave counts; layout: offsets + counts
+  const int tid = threadIdx.x;
+
+  if (static_cast<int32_t>(blockIdx.x) < num_chunks) {
+    // ---- place: copy -> row, stable inside each expert ----
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    for (int i = tid; i < kWaves * num_experts; i += kChunk) lds[i] = 0;
+    __syncthreads();
+
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kChunk + tid;
+    bool bad;
+    const int32_t e = read_expert(idx, c, n, k, num_experts, valid_tokens, &bad);
+    const bool valid = e >= 0;
+    const uint64_t peers = same_expert_lanes(valid, e, num_bits);
+    const uint64_t lower = peers & lanes_below();
+    if (valid && lower == 0) lds[wave * num_experts + e] = __popcll(peers);  // one writer per (wave, e)
+    __syncthreads();
+    (void)lane;
+
+    if (valid) {
+      int32_t before = 0;
+      for (int w = 0; w < wave; ++w) before += lds[w * num_experts + e];
+      const int32_t row = padded_offsets[e] +
+                          chunk_base[static_cast<int64_t>(blockIdx.x) * (num_experts + 1) + e] + before +
+                          __popcll(lower);
+      copy_row[c] = row;
+      row_token[row] = static_cast<int32_t>(c / k);
+    } else if (c < n) {
+      copy_row[c] = -1;
+    }
+    return;
+  }
+
+  // ---- layout: BSR arrays and the -1 marks of non-copy rows ----
+  int32_t* offs = lds;                    // [E+1] padded_offsets
+  int32_t* cnts = lds + kMaxExperts + 1;  // [E] tokens_per_expert (E <= 1024, fits the array)
+  for (int e = tid; e <= num_experts; e += kChunk) offs[e] = padded_offsets[e];
+  for (int e = tid; e < num_experts; e += kChunk) cnts[e] = tokens_per_expert[e];
+  __syncthreads();
+
+  const int32_t num_rows = offs[num_experts];
+  const int32_t num_row_blocks = num_rows / block_size;
+  // Last expert whose range starts at or before `row`: empty experts share a
+  // start with the next one, and "last" steps over them.
+  auto expert_of_row = [&](int32_t row) {
+    int32_t lo = 0, hi = num_experts - 1;
+    while (lo < hi) {
+      const int32_t mid = (lo + hi + 1) >> 1;
+      if (offs[mid] <= row) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
+
+  const int64_t i = static_cast<int64_t>(blockIdx.x - num_chunks) * kLayoutItemsPerGroup + tid;
+  const int64_t bsr_items = static_cast<int64_t>(max_row_blocks) * ffn_blocks;
+  if (i <= max_row_blocks) {
+    const int32_t r = static_cast<int32_t>(i);
+    row_offsets[r] = (r < num_row_blocks ? r : num_row_blocks) * ffn_blocks;
+  }
+  if (i < bsr_items) {
+    const int32_t r = static_cast<int32_t>(i / ffn_blocks);
+    const int32_t j = static_cast<int32_t>(i % ffn_blocks);
+    const int32_t expert = r < num_row_blocks ? expert_of_row(r * block_size) : -1;
+    col_indices[i] = expert < 0 ? -1 : expert * ffn_blocks + j;
+    if (j == 0) row_block_expert[r] = expert;
+  }
+  if (i < max_rows) {
+    const int32_t row = static_cast<int32_t>(i);
+    bool copy_here = false;
+    if (row < num_rows) {
+      const int32_t e = expert_of_row(row);
+      copy_here = row - offs[e] < cnts[e];
+    }
+    if (!copy_here) row_token[row] = -1;
+  }
+}
+
+int bits_for(int32_t num_experts) {
+  int b = 0;
+  while ((1 << b) < num_experts) ++b;
+  return b;
+}
+
+}  // namespace
+}  // namespace sb
+
+using namespace sb;
+
+extern "C" int sb_routing_sizes(int64_t num_copies, int32_t num_experts, int32_t ffn_dim, int32_t block_size,
+                                int64_t* max_row_blocks, int64_t* max_rows, int64_t* workspace_elems) {
+  constexpr int64_t kI32Max = 2147483647;
+  if (num_copies <= 0) return fail(SB_ERR_INVALID, "expert_idx must be [T, k] with T, k > 0");
+  if (num_experts <= 0 || num_experts > kMaxExperts)
+    return fail(SB_ERR_INVALID, "num_experts must be in [1, %d], got %d", kMaxExperts, num_experts);
+  if (block_size <= 0) return fail(SB_ERR_INVALID, "block_size must be in [1, 2^31)");
+  if (ffn_dim <= 0 || ffn_dim % block_size != 0)
+    return fail(SB_ERR_INVALID, "ffn_dim (%d) must be a positive multiple of block_size (%d)", ffn_dim, block_size);
+  if (num_copies > kI32Max) return fail(SB_ERR_INVALID, "problem too large for int32 indexing");
+  const int64_t rb = (num_copies + static_cast<int64_t>(num_experts) * (block_size - 1)) / block_size;
+  const int64_t rows = rb * block_size;
+  const int64_t ffn_blocks = ffn_dim / block_size;
+  if (rows > kI32Max / ffn_dim || rb * ffn_blocks >= kI32Max)
+    return fail(SB_ERR_INVALID, "problem too large for int32 indexing");
+  const int64_t chunks = (num_copies + kChunk - 1) / kChunk;
+  if (max_row_blocks) *max_row_blocks = rb;
+  if (max_rows) *max_rows = rows;
+  if (workspace_elems) *workspace_elems = chunks * (num_experts + 1);
+  return clear_ok();
+}
+
+extern "C" int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, int32_t k,
+                          int32_t num_experts, int32_t ffn_dim, int32_t block_size, const int32_t* valid_tokens,
+                          int32_t* workspace, int32_t* tokens_per_expert, int32_t* padded_offsets,
+                          int32_t* row_token, int32_t* copy_row, int32_t* row_block_expert, int32_t* row_offsets,
+                          int32_t* col_indices, int32_t* error, void* stream_ptr) {
+  if (num_tokens <= 0 || k <= 0) return fail(SB_ERR_INVALID, "expert_idx must be [T, k] with T, k > 0");
+  const int64_t n = num_tokens * k;
+  int64_t max_row_blocks = 0, max_rows = 0, ws = 0;
+  if (int rc = sb_routing_sizes(n, num_experts, ffn_dim, block_size, &max_row_blocks, &max_rows, &ws)) return rc;
+  if (!expert_idx || !workspace || !tokens_per_expert || !padded_offsets || !row_token || !copy_row ||
+      !row_block_expert || !row_offsets || !col_indices || !error)
+    return fail(SB_ERR_INVALID, "sb_routing: null buffer");
+
+  const hipStream_t stream = as_stream(stream_ptr);
+  const int32_t num_chunks = static_cast<int32_t>((n + kChunk - 1) / kChunk);
+  const int32_t ffn_blocks = ffn_dim / block_size;
+  const int num_bits = bits_for(num_experts);
+  const int64_t layout_items = std::max<int64_t>(max_row_blocks * ffn_blocks + 1, max_rows);
+  const int32_t layout_groups = static_cast<int32_t>((layout_items + kLayoutItemsPerGroup - 1) / kLayoutItemsPerGroup);
+
+  if (idx_is_i64) {
+    route_count_kernel<int64_t><<<num_chunks, kChunk, 0, stream>>>(
+        static_cast<const int64_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, workspace);
+  } else {
+    route_count_kernel<int32_t><<<num_chunks, kChunk, 0, stream>>>(
+        static_cast<const int32_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, workspace);
+  }
+  if (int rc = check_launch("routing count")) return rc;
+
+  route_offsets_kernel<<<1, kChunk, 0, stream>>>(workspace, num_chunks, num_experts, block_size, tokens_per_expert,
+                                                 padded_offsets, error);
+  if (int rc = check_launch("routing offsets")) return rc;
+
+  const int32_t grid = num_chunks + layout_groups;
+  if (idx_is_i64) {
+    route_place_kernel<int64_t><<<grid, kChunk, 0, stream>>>(
+        static_cast<const int64_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, num_chunks, workspace,
+        tokens_per_expert, padded_offsets, block_size, ffn_blocks, static_cast<int32_t>(max_row_blocks), max_rows,
+        copy_row, row_token, row_block_expert, row_offsets, col_indices);
+  } else {
+    route_place_kernel<int32_t><<<grid, kChunk, 0, stream>>>(
+        static_cast<const int32_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, num_chunks, workspace,
+        tokens_per_expert, padded_offsets, block_size, ffn_blocks, static_cast<int32_t>(max_row_blocks), max_rows,
+        copy_row, row_token, row_block_expert, row_offsets, col_indices);
+  }
+  if (int rc = check_launch("routing place")) return rc;
+  return clear_ok();
+}

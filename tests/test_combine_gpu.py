@@ -1,0 +1,71 @@
+"""The combine kernel against the closed form (fp32 products summed over k).
+
+The kernel rounds one fp32 sum per element to bf16, like the oracle does
+after its fp32 sum, so the two agree to one bf16 rounding step plus fp32
+summation order: rtol 1e-2, atol 1e-5.
+"""
+
+import pytest
+import torch
+
+from oracle.moe_ref import combine_reference
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"rtol": 1e-2, "atol": 1e-5}
+
+
+def make(num_tokens: int, k: int, d_model: int, rows: int, gate_dtype, seed: int = 0, skipped: float = 0.0):
+    g = torch.Generator().manual_seed(seed)
+    y = torch.randn(rows, d_model, generator=g).bfloat16()
+    copy_row = torch.randperm(rows, generator=g)[: num_tokens * k].int()
+    if skipped:
+        drop = torch.rand(num_tokens * k, generator=g) < skipped
+        copy_row[drop] = -1
+    w = torch.rand(num_tokens, k, generator=g).to(gate_dtype)
+    return y, copy_row, w
+
+
+@pytest.mark.parametrize("gate_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("num_tokens", "k", "d_model"), [(1, 1, 8), (300, 2, 256), (77, 4, 1024), (4096, 2, 1024)])
+def test_matches_closed_form(gate_dtype, num_tokens, k, d_model) -> None:
+    from sparsebench_amd.moe import combine
+
+    y, copy_row, w = make(num_tokens, k, d_model, num_tokens * k + 37, gate_dtype)
+    out = combine(y.cuda(), copy_row.cuda(), w.cuda())
+    assert out.dtype == torch.bfloat16 and out.shape == (num_tokens, d_model)
+    torch.testing.assert_close(out.float().cpu(), combine_reference(y, copy_row.numpy(), w), **TOL)
+
+
+def test_skipped_copies_add_nothing() -> None:
+    from sparsebench_amd.moe import combine
+
+    y, copy_row, w = make(500, 2, 128, 1100, torch.float32, skipped=0.3)
+    out = combine(y.cuda(), copy_row.cuda(), w.cuda())
+    torch.testing.assert_close(out.float().cpu(), combine_reference(y, copy_row.numpy(), w), **TOL)
+    both = (copy_row.view(500, 2) < 0).all(dim=1)
+    assert torch.all(out.cpu()[both] == 0)
+
+
+def test_exact_on_representable_values() -> None:
+    # Gates of 1 and 0.5 and small integer-valued rows: every product and sum
+    # is exact in fp32 and representable in bf16, so the result is bit-exact.
+    from sparsebench_amd.moe import combine
+
+    y = torch.arange(-64, 64, dtype=torch.float32).repeat(6, 1).bfloat16()  # [6, 128]
+    copy_row = torch.tensor([5, 0, 1, 4, 2, 3], dtype=torch.int32)
+    w = torch.tensor([[1.0, 0.5], [0.5, 0.5], [1.0, 1.0]])
+    out = combine(y.cuda(), copy_row.cuda(), w.cuda()).float().cpu()
+    expected = combine_reference(y, copy_row.numpy(), w)
+    assert torch.equal(out, expected)
+
+
+def test_valid_tokens_stops_at_the_device_count() -> None:
+    from sparsebench_amd import _C
+
+    y, copy_row, w = make(64, 2, 64, 200, torch.float32)
+    vt = torch.tensor([40], dtype=torch.int32, device="cuda")
+    out = _C.combine_cuda(y.cuda(), copy_row.cuda(), w.cuda(), vt)
+    torch.testing.assert_close(out[:40].float().cpu(), combine_reference(y, copy_row.numpy(), w)[:40], **TOL)
+    full = _C.combine_cuda(y.cuda(), copy_row.cuda(), w.cuda())
+    assert torch.equal(out[:40], full[:40])

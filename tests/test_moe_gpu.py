@@ -1,0 +1,149 @@
+"""The whole layer (routing -> SDD+GELU -> DSD -> combine) against the fp32
+loop reference on the same bf16 values (the reference's tests/test_moe.py).
+
+Gates: max |out - ref| / max |ref| <= 2e-2, and the reference's own
+assert_close(rtol=3e-2, atol=3e-2). H is rounded to bf16 between the two
+matmuls, as in any bf16 MoE, hence the wider bound than a single GEMM.
+"""
+
+import pytest
+import torch
+
+from oracle.moe_ref import layer_reference_fp32, max_rel_err, route
+from sparsebench_amd.workloads import CASE_NAMES, LayerShape, make_layer, routing_case, softmax_gates
+
+pytestmark = pytest.mark.gpu
+
+REL = 2e-2
+
+
+def small_layer(num_tokens: int, num_experts: int, d_model: int, ffn_dim: int, seed: int = 0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(num_tokens, d_model, generator=g).bfloat16().cuda()
+    w1 = (torch.randn(num_experts, d_model, ffn_dim, generator=g) / d_model**0.5).bfloat16().cuda()
+    w2 = (torch.randn(num_experts, ffn_dim, d_model, generator=g) / ffn_dim**0.5).bfloat16().cuda()
+    return x, w1, w2
+
+
+def check(out, x, idx, weight, w1, w2) -> None:
+    expected = layer_reference_fp32(x, idx, weight, w1, w2)
+    assert out.dtype == torch.bfloat16 and out.shape == x.shape
+    assert max_rel_err(out, expected) <= REL
+    torch.testing.assert_close(out.float().cpu(), expected, rtol=3e-2, atol=3e-2)
+
+
+@pytest.mark.parametrize("case", CASE_NAMES)
+@pytest.mark.parametrize(("num_experts", "d_model", "ffn_dim"), [(8, 256, 512), (64, 256, 256)], ids=["E8", "E64"])
+def test_layer_matches_reference(case: str, num_experts: int, d_model: int, ffn_dim: int) -> None:
+    from sparsebench_amd.moe import moe_forward
+
+    x, w1, w2 = small_layer(300, num_experts, d_model, ffn_dim)
+    idx = routing_case(case, 300, num_experts).cuda()
+    weight = torch.rand(300, 2, generator=torch.Generator().manual_seed(1)).bfloat16().cuda()
+    check(moe_forward(x, idx, weight, w1, w2), x, idx, weight, w1, w2)
+
+
+def test_layer_with_router() -> None:
+    from sparsebench_amd.moe import moe_forward
+
+    x, w1, w2 = small_layer(500, 8, 256, 512)
+    logits = x.float().cpu() @ torch.randn(256, 8, generator=torch.Generator().manual_seed(2))
+    idx, weight = route(logits)
+    idx, weight = idx.cuda(), weight.bfloat16().cuda()
+    check(moe_forward(x, idx, weight, w1, w2), x, idx, weight, w1, w2)
+
+
+@pytest.mark.parametrize("routing", ["random", "zipf_perm"])
+def test_fine_grained_config(routing: str) -> None:
+    # The benchmark's fine-grained shape at full size: T=4096, D=1024, F=4096, E=64, top-2.
+    from sparsebench_amd.moe import moe_forward
+
+    shape = LayerShape("fine_grained", 4096, 1024, 4096, 64)
+    x, idx, gates, w1, w2 = make_layer(shape, routing, seed=0)
+    out = moe_forward(x, idx, gates, w1, w2)
+    check(out, x, idx, gates, w1, w2)
+
+
+def test_graph_capture_and_replay_with_new_tokens_and_routing() -> None:
+    # Capture fails on any host sync; each replay reads fresh x and routing.
+    from sparsebench_amd.moe import moe_forward
+
+    num_tokens, num_experts, d_model, ffn_dim = 512, 16, 256, 256
+    x, w1, w2 = small_layer(num_tokens, num_experts, d_model, ffn_dim)
+    idx = routing_case("random", num_tokens, num_experts, seed=1).cuda()
+    weight = softmax_gates(num_tokens, 2, seed=1, device="cuda").bfloat16()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe_forward(x, idx, weight, w1, w2)
+    torch.cuda.current_stream().wait_stream(side)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = moe_forward(x, idx, weight, w1, w2)
+
+    for seed, case in [(2, "zipf"), (3, "empty_middle"), (4, "skewed"), (5, "random")]:
+        new_x, _, _ = small_layer(num_tokens, num_experts, d_model, ffn_dim, seed=seed)
+        x.copy_(new_x)
+        idx.copy_(routing_case(case, num_tokens, num_experts, seed=seed).cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        check(out, x, idx, weight, w1, w2)
+        eager = moe_forward(x, idx, weight, w1, w2)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, out)
+
+
+def test_graph_replay_at_fewer_tokens() -> None:
+    # Captured once with buffers for T_max; the token count is a device scalar.
+    from sparsebench_amd.moe import moe_forward
+
+    t_max, num_experts, d_model, ffn_dim = 2048, 32, 256, 256
+    x, w1, w2 = small_layer(t_max, num_experts, d_model, ffn_dim)
+    idx = routing_case("zipf_perm", t_max, num_experts, seed=1).cuda()
+    weight = softmax_gates(t_max, 2, seed=1, device="cuda")
+    valid = torch.tensor([t_max], dtype=torch.int32, device="cuda")
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe_forward(x, idx, weight, w1, w2, valid_tokens=valid)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = moe_forward(x, idx, weight, w1, w2, valid_tokens=valid)
+
+    for seed, t in [(2, 100), (3, 2048), (4, 777), (5, 1)]:
+        new_x, _, _ = small_layer(t_max, num_experts, d_model, ffn_dim, seed=seed)
+        x.copy_(new_x)
+        idx.copy_(routing_case("zipf_perm", t_max, num_experts, seed=seed).cuda())
+        valid.fill_(t)
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = layer_reference_fp32(x[:t], idx[:t], weight[:t], w1, w2)
+        assert max_rel_err(out[:t], expected) <= REL
+
+
+def test_stage_marks_fire_in_order_and_change_nothing() -> None:
+    from sparsebench_amd.moe import moe_forward
+
+    x, w1, w2 = small_layer(300, 8, 256, 512)
+    idx = routing_case("zipf", 300, 8).cuda()
+    weight = torch.rand(300, 2, generator=torch.Generator().manual_seed(1)).bfloat16().cuda()
+    seen: list[str] = []
+    marked = moe_forward(x, idx, weight, w1, w2, mark=seen.append)
+    assert seen == ["routing", "SDD + GELU (fused)", "DSD", "combine"]
+    assert torch.equal(marked, moe_forward(x, idx, weight, w1, w2))
+
+
+def test_rejects_mismatched_shapes() -> None:
+    from sparsebench_amd.moe import moe_forward
+
+    x, w1, w2 = small_layer(10, 4, 256, 256)
+    idx = routing_case("random", 10, 4).cuda()
+    weight = torch.ones(10, 2, device="cuda")
+    with pytest.raises(ValueError, match="w2"):
+        moe_forward(x, idx, weight, w1, w2[:, :128])
+    with pytest.raises(ValueError, match="x must be"):
+        moe_forward(x, idx, weight[:, :1], w1, w2)

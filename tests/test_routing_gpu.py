@@ -1,0 +1,161 @@
+"""GPU routing is bit-exact to the layout oracle, every element of every
+worst-case buffer (the grid of the reference's tests/test_routing.py)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.topology_ref import build_layout, device_layout
+from sparsebench_amd.workloads import CASE_NAMES, routing_case
+
+pytestmark = pytest.mark.gpu
+
+FIELDS = ("tokens_per_expert", "padded_offsets", "row_token", "copy_row", "row_block_expert", "row_offsets",
+          "col_indices")
+
+
+def route(expert_idx: torch.Tensor, num_experts: int, ffn_dim: int, block_size: int, valid_tokens=None):
+    from sparsebench_amd.routing import route_device
+
+    return route_device(expert_idx.cuda(), num_experts, ffn_dim, block_size, valid_tokens)
+
+
+def assert_device_matches(dev, expected) -> None:
+    for f in FIELDS:
+        got = getattr(dev, f)
+        assert got.dtype == torch.int32 and got.is_cuda, f
+        np.testing.assert_array_equal(got.cpu().numpy(), getattr(expected, f), err_msg=f)
+    assert int(dev.error.item()) == expected.error
+
+
+def check(expert_idx: torch.Tensor, num_experts: int, block_size: int, ffn_dim: int | None = None) -> None:
+    ffn_dim = ffn_dim or 2 * block_size
+    dev = route(expert_idx, num_experts, ffn_dim, block_size)
+    assert_device_matches(dev, device_layout(expert_idx.numpy(), num_experts, ffn_dim, block_size))
+    # The trimmed Topology equals the reference's build_topology layout.
+    topo = dev.to_topology()
+    lay = build_layout(expert_idx.numpy(), num_experts, ffn_dim, block_size)
+    for f in FIELDS:
+        np.testing.assert_array_equal(getattr(topo, f).cpu().numpy(), getattr(lay, f), err_msg=f)
+
+
+@pytest.mark.parametrize("case", CASE_NAMES)
+@pytest.mark.parametrize("num_experts", [2, 8, 64, 256])
+@pytest.mark.parametrize("block_size", [4, 16, 128])
+@pytest.mark.parametrize("num_tokens", [1, 13, 129, 1000])
+def test_matches_oracle(case: str, num_experts: int, block_size: int, num_tokens: int) -> None:
+    check(routing_case(case, num_tokens, num_experts), num_experts, block_size)
+
+
+@pytest.mark.parametrize("k", [1, 2, 4])
+@pytest.mark.parametrize("num_tokens", [1, 77, 3000])
+def test_matches_oracle_any_k(k: int, num_tokens: int) -> None:
+    check(routing_case("random", num_tokens, 16, k=k), 16, 16)
+
+
+@pytest.mark.parametrize("case", ["random", "skewed", "zipf"])
+@pytest.mark.parametrize("num_experts", [8, 1024])
+def test_matches_oracle_big(case: str, num_experts: int) -> None:
+    # 200k copies: 196 chunks of 1024, a long walk in the offsets kernel.
+    check(routing_case(case, 100_000, num_experts), num_experts, 128)
+
+
+@pytest.mark.parametrize("num_experts", [1, 3, 1023])
+def test_odd_expert_counts(num_experts: int) -> None:
+    g = torch.Generator().manual_seed(11)
+    check(torch.randint(0, num_experts, (2500, 2), generator=g), num_experts, 16)
+
+
+@pytest.mark.parametrize("case", ["random", "zipf_perm"])
+def test_fine_grained_shape(case: str) -> None:
+    # The benchmark shape: 4096 tokens, top-2, 64 experts, F = 4096.
+    check(routing_case(case, 4096, 64), 64, 128, ffn_dim=4096)
+
+
+def test_int32_and_int64_input_agree() -> None:
+    idx = routing_case("random", 500, 8)
+    a, b = route(idx.int(), 8, 32, 16), route(idx, 8, 32, 16)
+    for f in FIELDS:
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+
+
+def test_deterministic() -> None:
+    idx = routing_case("skewed", 5000, 64)
+    a, b = route(idx, 64, 256, 128), route(idx, 64, 256, 128)
+    for f in FIELDS:
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+
+
+def test_worst_case_buffers_are_marked_past_the_end() -> None:
+    dev = route(routing_case("random", 100, 8), 8, 32, 16)
+    num_rows = int(dev.padded_offsets[-1])
+    nrb = num_rows // 16
+    assert torch.all(dev.row_token[num_rows:] == -1)
+    assert torch.all(dev.row_block_expert[nrb:] == -1)
+    assert torch.all(dev.col_indices[nrb * 2:] == -1)
+    assert torch.all(dev.row_offsets[nrb:] == nrb * 2)
+
+
+def test_graph_capture_proves_no_host_sync() -> None:
+    # Capture fails if anything waits on the GPU; replaying with new routing
+    # proves the graph reads its input instead of a baked-in result. Each
+    # replay is checked, with eager work and syncs in between.
+    from sparsebench_amd.routing import route_device
+
+    num_tokens, num_experts, ffn_dim, bs = 4000, 32, 256, 128
+    static_idx = routing_case("random", num_tokens, num_experts, seed=1).cuda()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        route_device(static_idx, num_experts, ffn_dim, bs)
+    torch.cuda.current_stream().wait_stream(side)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = route_device(static_idx, num_experts, ffn_dim, bs)
+
+    for case, seed in [("skewed", 2), ("empty_middle", 2), ("zipf", 3), ("random", 4)]:
+        new_idx = routing_case(case, num_tokens, num_experts, seed=seed)
+        static_idx.copy_(new_idx)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_device_matches(captured, device_layout(new_idx.numpy(), num_experts, ffn_dim, bs))
+        route_device(static_idx, num_experts, ffn_dim, bs)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_out_of_range_id_is_skipped_and_flagged() -> None:
+    from sparsebench_amd.routing import route_device
+
+    dev = route_device(torch.tensor([[0, 1], [2, 8], [-1, 3]], device="cuda"), 8, 32, 16)
+    with pytest.raises(ValueError, match="outside"):
+        dev.to_topology()
+    assert int(dev.tokens_per_expert.sum()) == 4
+    assert dev.copy_row.tolist() == [0, 16, 32, -1, -1, 48]
+
+
+@pytest.mark.parametrize("valid", [1, 700, 2047, 2048])
+def test_valid_tokens_matches_truncated_oracle(valid: int) -> None:
+    idx = routing_case("zipf_perm", 2048, 128)
+    vt = torch.tensor([valid], dtype=torch.int32, device="cuda")
+    dev = route(idx, 128, 768, 128, valid_tokens=vt)
+    assert_device_matches(dev, device_layout(idx.numpy(), 128, 768, 128, valid_tokens=valid))
+
+
+BAD_INPUTS = {
+    "cpu_tensor": (lambda: torch.tensor([[0, 1]]), 8, 32, "CUDA"),
+    "not_2d": (lambda: torch.tensor([0, 1], device="cuda"), 8, 32, r"\[T, k\]"),
+    "too_many_experts": (lambda: torch.tensor([[0, 1]], device="cuda"), 2000, 32, "num_experts"),
+    "ffn_not_multiple": (lambda: torch.tensor([[0, 1]], device="cuda"), 8, 30, "multiple"),
+    "float_ids": (lambda: torch.tensor([[0.0, 1.0]], device="cuda"), 8, 32, "int32"),
+    "not_contiguous": (lambda: torch.zeros(4, 4, dtype=torch.long, device="cuda")[:, ::2], 8, 32, "contiguous"),
+}
+
+
+@pytest.mark.parametrize("name", BAD_INPUTS)
+def test_rejects_bad_input(name: str) -> None:
+    from sparsebench_amd.routing import build_topology_cuda
+
+    make, num_experts, ffn_dim, match = BAD_INPUTS[name]
+    with pytest.raises(RuntimeError, match=match):
+        build_topology_cuda(make(), num_experts, ffn_dim, 16)

@@ -1,0 +1,124 @@
+"""SDD (x gathered @ W1 -> GELU -> BSR blocks) against the fp32 oracle
+(the cases of the reference's tests/test_sdd.py).
+
+Tolerance: rtol = atol = 1.6e-2, the reference's bf16-output bound (the
+kernel rounds each fp32 result once to bf16; layout bugs are far larger).
+"""
+
+import pytest
+import torch
+
+from oracle.moe_ref import sdd_blocks
+from oracle.topology_ref import build_layout, device_layout
+from sparsebench_amd.workloads import CASE_NAMES, routing_case
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"rtol": 1.6e-2, "atol": 1.6e-2}
+
+
+def make_inputs(case: str, num_tokens: int, num_experts: int, d_model: int, ffn_dim: int, seed: int = 0):
+    g = torch.Generator().manual_seed(seed)
+    idx = routing_case(case, num_tokens, num_experts, seed)
+    x = torch.randn(num_tokens, d_model, generator=g).bfloat16()
+    w1 = (torch.randn(num_experts, d_model, ffn_dim, generator=g) / d_model**0.5).bfloat16()
+    return idx, x, w1
+
+
+def expected(idx, x, w1, gelu: bool = True, block_size: int = 128) -> torch.Tensor:
+    lay = build_layout(idx.numpy(), w1.shape[0], w1.shape[2], block_size)
+    return sdd_blocks(x.float(), w1.float(), lay, gelu)
+
+
+def run_sdd(idx, x, w1, gelu: bool = True):
+    from sparsebench_amd.routing import build_topology_cuda
+    from sparsebench_amd.spmm import sdd
+
+    topo = build_topology_cuda(idx.cuda(), w1.shape[0], w1.shape[2], 128)
+    return sdd(x.cuda(), w1.cuda(), topo, gelu=gelu)
+
+
+@pytest.mark.parametrize("case", CASE_NAMES)
+@pytest.mark.parametrize(("num_experts", "d_model", "ffn_dim"),
+                         [(8, 128, 256), (8, 320, 512), (64, 64, 256), (4, 1024, 4096)],
+                         ids=["E8D128F256", "E8D320F512", "E64D64F256", "E4D1024F4096"])
+def test_sdd_matches_oracle(case: str, num_experts: int, d_model: int, ffn_dim: int) -> None:
+    idx, x, w1 = make_inputs(case, 300, num_experts, d_model, ffn_dim)
+    torch.testing.assert_close(run_sdd(idx, x, w1).float().cpu(), expected(idx, x, w1), **TOL)
+
+
+def test_sdd_without_gelu() -> None:
+    idx, x, w1 = make_inputs("zipf", 200, 8, 128, 256)
+    torch.testing.assert_close(run_sdd(idx, x, w1, gelu=False).float().cpu(), expected(idx, x, w1, False), **TOL)
+
+
+def test_sdd_single_token_is_mostly_padding() -> None:
+    # 1 token, 2 copies: each row block is 1 real row + 127 zero rows.
+    idx, x, w1 = make_inputs("random", 1, 8, 128, 256)
+    out = run_sdd(idx, x, w1, gelu=False).float().cpu()
+    torch.testing.assert_close(out, expected(idx, x, w1, False), **TOL)
+    assert torch.all(out[:, 1:, :] == 0), "padding rows must come out exactly zero"
+
+
+def test_sdd_asymmetric_inputs() -> None:
+    # Structured values with no symmetry between rows, columns, x and W, so a
+    # transposed or swapped fragment cannot hide behind random data.
+    idx = routing_case("random", 200, 4)
+    t = torch.arange(200, dtype=torch.float32)[:, None]
+    d = torch.arange(256, dtype=torch.float32)[None, :]
+    x = torch.sin(0.37 * t + 1.31 * d + 0.05 * t * d / 256).bfloat16()
+    e = torch.arange(4, dtype=torch.float32)[:, None, None]
+    dd = torch.arange(256, dtype=torch.float32)[None, :, None]
+    f = torch.arange(512, dtype=torch.float32)[None, None, :]
+    w1 = (torch.cos(0.7 * dd - 0.23 * f + 0.11 * e + 0.01 * dd * f / 512) / 16).bfloat16()
+    torch.testing.assert_close(run_sdd(idx, x, w1).float().cpu(), expected(idx, x, w1), **TOL)
+
+
+def test_sdd_worst_case_device_topology() -> None:
+    from sparsebench_amd.routing import route_device
+    from sparsebench_amd.spmm import sdd
+
+    idx, x, w1 = make_inputs("zipf", 400, 64, 128, 256)
+    dev = route_device(idx.cuda(), 64, 256, 128)
+    out = sdd(x.cuda(), w1.cuda(), dev)
+    topo = dev.to_topology()
+    assert out.shape[0] == dev.col_indices.numel()
+    torch.testing.assert_close(out[: topo.nnz_blocks].float().cpu(), expected(idx, x, w1), **TOL)
+
+
+def test_sdd_wide_tiles() -> None:
+    # Enough row blocks that the 256-column tile path runs (>= 1024 tiles).
+    idx, x, w1 = make_inputs("random", 4096, 64, 128, 4096, seed=2)
+    dev_lay = device_layout(idx.numpy(), 64, 4096, 128)
+    assert (dev_lay.row_block_expert.size * 16) >= 1024
+    torch.testing.assert_close(run_sdd(idx, x, w1).float().cpu(), expected(idx, x, w1), **TOL)
+
+
+BAD = {
+    "fp32_x": (lambda x, w1: (x.float(), w1), "bfloat16"),
+    "f_not_256": (lambda x, w1: (x, w1[:, :, :128].contiguous()), "multiple of 256"),
+    "d_not_64": (lambda x, w1: (x[:, :96].contiguous(), w1[:, :96].contiguous()), "multiple of 64"),
+    "d_mismatch": (lambda x, w1: (x[:, :64].contiguous(), w1), r"\[T, D\]"),
+}
+
+
+@pytest.mark.parametrize("name", BAD)
+def test_sdd_rejects_bad_input(name: str) -> None:
+    from sparsebench_amd import _C
+    from sparsebench_amd.routing import build_topology_cuda
+
+    idx, x, w1 = make_inputs("random", 20, 4, 128, 256)
+    topo = build_topology_cuda(idx.cuda(), 4, 256, 128)
+    change, match = BAD[name]
+    xx, ww = change(x.cuda(), w1.cuda())
+    with pytest.raises(RuntimeError, match=match):
+        _C.sdd_cuda(xx, ww, topo.row_token, topo.row_block_expert, topo.row_offsets, topo.col_indices.numel(), True)
+
+
+def test_sdd_rejects_block_size_64() -> None:
+    from sparsebench_amd.routing import build_topology_cuda
+    from sparsebench_amd.spmm import sdd
+
+    idx, x, w1 = make_inputs("random", 20, 4, 128, 256)
+    with pytest.raises(ValueError, match="block size 128"):
+        sdd(x.cuda(), w1.cuda(), build_topology_cuda(idx.cuda(), 4, 256, 64))

@@ -243,14 +243,14 @@ def main() -> int:
         if hbm_bound:
             achieved = nbytes[name] / (kms * 1e-3) / 1e9
             roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": f"{name}_kernel",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": f"{name} stage (one kernel)",
                         "algorithmic_bytes": nbytes[name], "kernel_ms": kms,
                         "useful_tflops": round(flops / (kms * 1e-3) / 1e12, 2)}
         else:
             achieved = flops / (kms * 1e-3) / 1e12
             roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                        "kernel": f"{name}_kernel", "useful_flops": flops, "kernel_ms": kms}
+                        "kernel": f"{name} stage (one kernel)", "useful_flops": flops, "kernel_ms": kms}
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <algorithm>
 #include <string>
 #include <type_traits>
@@ -34,6 +35,19 @@ inline int check_launch(const char* what) {
   return SB_OK;
 }
 
+// Kernel-variant override from the environment, for tuning sweeps (read on
+// every call); 0 when unset, which selects the built-in choice.
+inline int tuning_override(const char* name) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : 0;
+}
+
+// Row blocks per tile group (see tile_coords).
+inline int tile_group() {
+  const int forced = tuning_override("SPARSEBENCH_TILE_GROUP");
+  return forced > 0 ? forced : 8;
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -42,15 +56,14 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
-// Round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
+typedef __bf16 bf16x2_pack_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16, round to nearest even, NaN kept (gfx950's v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const bf16x2_pack_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // ------------------------------------------------------------ scheduling ---
@@ -69,6 +82,26 @@ __device__ __forceinline__ int xcd_remap(int bid, int live) {
   const int x = bid % kNumXcd;
   const int q = bid / kNumXcd;
   return x < rem ? x * (per + 1) + q : rem * (per + 1) + (x - rem) * per + q;
+}
+
+// Logical tile -> (row block, column slice) for the live region: tiles are
+// taken in groups of `group` row blocks, walking down the group one column
+// slice at a time, so the tiles that run together on one XCD cover a few
+// row blocks x a few slices and share both their A rows and their W columns
+// in that XCD's L2. Tiles past the live region map row block first.
+__device__ __forceinline__ void tile_coords(int tile, int live_rb, int slices, int group, int* rb, int* slice) {
+  if (tile >= live_rb * slices || group <= 1) {
+    *rb = tile / slices;
+    *slice = tile % slices;
+    return;
+  }
+  const int per_group = group * slices;
+  const int g = tile / per_group;
+  const int first = g * group;
+  const int size = min(group, live_rb - first);
+  const int local = tile - g * per_group;
+  *rb = first + local % size;
+  *slice = local / size;
 }
 
 // Number of leading row blocks that can hold work. The routing layout puts

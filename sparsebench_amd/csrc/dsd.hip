@@ -13,6 +13,7 @@
 
 #include <type_traits>
 
+#include "gemm_dma.hpp"
 #include "gemm_tile.hpp"
 
 namespace sb {
@@ -61,20 +62,21 @@ struct DsdLoader {
   }
 };
 
-template <int BM, int BN>
-__global__ void __launch_bounds__(256)
+template <class Cfg>
+__global__ void __launch_bounds__(Cfg::kThreads)
     dsd_kernel(const uint16_t* __restrict__ blocks, const uint16_t* __restrict__ w,
                const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ col_indices,
                uint16_t* __restrict__ out, int64_t nnz, int64_t w_rows, int32_t num_row_blocks, int32_t d_model,
-               int32_t num_slices, int32_t zero_dead_rows) {
-  using Cfg = TileCfg<BM, BN>;
+               int32_t num_slices, int32_t zero_dead_rows, int32_t group) {
   using ML = Mainloop<Cfg>;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN;
   __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::kLdsElems];
 
-  const int live = (zero_dead_rows ? num_row_blocks : live_row_blocks(row_offsets, num_row_blocks)) * num_slices;
-  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live);
-  const int rb = tile / num_slices;
-  const int n0 = (tile % num_slices) * BN;
+  const int live_rb = zero_dead_rows ? num_row_blocks : live_row_blocks(row_offsets, num_row_blocks);
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
+  int rb, slice;
+  tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
+  const int n0 = slice * BN;
   int32_t begin = row_offsets[rb];
   int32_t end = row_offsets[rb + 1];
   if (begin < 0 || end > nnz || end < begin) begin = end = 0;  // not a BSR row: treat as empty
@@ -112,17 +114,152 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-template <int BM, int BN>
+// The same tile on the LDS-DMA mainloop (gemm_dma.hpp). A block of w that
+// does not exist (bad column index) gets a zero-length buffer: its loads
+// return zeros and it contributes nothing.
+template <class Cfg>
+struct DsdDmaSrc {
+  static constexpr int kStepsPerBlock = Cfg::BM / Cfg::BK;
+  const uint16_t* blocks;
+  const uint16_t* w;
+  const int32_t* col_indices;
+  int64_t w_rows;
+  int32_t d_model, begin;
+  uint32_t a_voff[Cfg::kAInstr];
+  uint32_t b_voff[Cfg::kBInstr];
+  __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    const int32_t p = begin + t / kStepsPerBlock;
+    *r = make_rsrc(blocks + static_cast<int64_t>(p) * Cfg::BM * Cfg::BM, Cfg::BM * Cfg::BM * 2);
+    *s = static_cast<uint32_t>(t % kStepsPerBlock) * (Cfg::BK * 2);
+  }
+  __device__ __forceinline__ void b_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    const int32_t p = begin + t / kStepsPerBlock;
+    const int64_t row0 = static_cast<int64_t>(col_indices[p]) * Cfg::BM;
+    const bool ok = row0 >= 0 && row0 + Cfg::BM <= w_rows;
+    *r = make_rsrc(w + (ok ? row0 : 0) * d_model, ok ? static_cast<uint32_t>(Cfg::BM) * d_model * 2u : 0u);
+    *s = static_cast<uint32_t>(t % kStepsPerBlock) * (Cfg::BK * 2u) * static_cast<uint32_t>(d_model);
+  }
+};
+
+template <class Cfg>
+__global__ void __launch_bounds__(Cfg::kThreads)
+    dsd_dma_kernel(const uint16_t* __restrict__ blocks, const uint16_t* __restrict__ w,
+                   const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ col_indices,
+                   uint16_t* __restrict__ out, int64_t nnz, int64_t w_rows, int32_t num_row_blocks, int32_t d_model,
+                   int32_t num_slices, int32_t zero_dead_rows, int32_t group) {
+  using ML = DmaMainloop<Cfg>;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+
+  const int live_rb = zero_dead_rows ? num_row_blocks : live_row_blocks(row_offsets, num_row_blocks);
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
+  int rb, slice;
+  tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
+  const int n0 = slice * BN;
+  int32_t begin = row_offsets[rb];
+  int32_t end = row_offsets[rb + 1];
+  if (begin < 0 || end > nnz || end < begin) begin = end = 0;  // not a BSR row: treat as empty
+
+  uint16_t* out_tile = out + static_cast<int64_t>(rb) * BM * d_model + n0;
+  if (begin == end) {
+    if (!zero_dead_rows) return;
+    constexpr int kChunksPerRow = BN / 8;
+    for (int q = threadIdx.x; q < BM * kChunksPerRow; q += Cfg::kThreads) {
+      const int r = q / kChunksPerRow, c = q % kChunksPerRow;
+      *reinterpret_cast<u32x4_t*>(out_tile + static_cast<int64_t>(r) * d_model + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+
+  DsdDmaSrc<Cfg> src;
+  src.blocks = blocks;
+  src.w = w + n0;
+  src.col_indices = col_indices;
+  src.w_rows = w_rows;
+  src.d_model = d_model;
+  src.begin = begin;
+  const ADmaPos<Cfg> ap;
+#pragma unroll
+  for (int q = 0; q < Cfg::kAInstr; ++q) src.a_voff[q] = (ap.row[q] * BM + ap.chunk[q] * 8) * 2u;
+  const BDmaPos<Cfg> bp;
+#pragma unroll
+  for (int q = 0; q < Cfg::kBInstr; ++q)
+    src.b_voff[q] = (static_cast<uint32_t>(bp.row[q]) * d_model + bp.col[q]) * 2u;
+
+  typename ML::Acc acc;
+  ML::run(lds, src, (end - begin) * DsdDmaSrc<Cfg>::kStepsPerBlock, acc);
+
+#pragma unroll
+  for (int jn = 0; jn < Cfg::TN; ++jn)
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; ++i) {
+      uint16_t* row = out_tile + static_cast<int64_t>(ML::out_row(i)) * d_model;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x16_t& a = acc[jn][i];
+        *reinterpret_cast<u32x2_t*>(row + ML::out_col(jn, g)) =
+            u32x2_t{pack_bf16x2(a[4 * g], a[4 * g + 1]), pack_bf16x2(a[4 * g + 2], a[4 * g + 3])};
+      }
+    }
+}
+
+template <class Cfg>
+int launch_dsd_dma(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices,
+                   void* out, int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t d_model,
+                   int32_t zero_dead_rows, hipStream_t stream) {
+  if (d_model % Cfg::BN != 0) return fail(SB_ERR_INVALID, "dsd: D %% tile width != 0");
+  const int32_t num_slices = static_cast<int32_t>(d_model / Cfg::BN);
+  const int64_t tiles = num_row_blocks * num_slices;
+  dsd_dma_kernel<Cfg><<<static_cast<uint32_t>(tiles), Cfg::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(blocks), static_cast<const uint16_t*>(w), row_offsets, col_indices,
+      static_cast<uint16_t*>(out), nnz, w_rows, static_cast<int32_t>(num_row_blocks), static_cast<int32_t>(d_model),
+      num_slices, zero_dead_rows, tile_group());
+  return check_launch("dsd");
+}
+
+template <class Cfg>
 int launch_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices, void* out,
                int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t d_model, int32_t zero_dead_rows,
                hipStream_t stream) {
-  const int32_t num_slices = static_cast<int32_t>(d_model / BN);
+  if (d_model % Cfg::BN != 0) return fail(SB_ERR_INVALID, "dsd: D %% tile width != 0");
+  const int32_t num_slices = static_cast<int32_t>(d_model / Cfg::BN);
   const int64_t tiles = num_row_blocks * num_slices;
-  dsd_kernel<BM, BN><<<static_cast<uint32_t>(tiles), 256, 0, stream>>>(
+  dsd_kernel<Cfg><<<static_cast<uint32_t>(tiles), Cfg::kThreads, 0, stream>>>(
       static_cast<const uint16_t*>(blocks), static_cast<const uint16_t*>(w), row_offsets, col_indices,
       static_cast<uint16_t*>(out), nnz, w_rows, static_cast<int32_t>(num_row_blocks), static_cast<int32_t>(d_model),
-      num_slices, zero_dead_rows);
+      num_slices, zero_dead_rows, tile_group());
   return check_launch("dsd");
+}
+
+// Tile variants (BN, waves WM x WN, register prefetch depth) for a block size BM.
+template <int BM, class... Args>
+int dispatch_dsd(int variant, Args... args) {
+  switch (variant) {
+    case 1: return launch_dsd<TileCfg<BM, 128, 2, 2, 1>>(args...);
+    case 2: return launch_dsd<TileCfg<BM, 256, 2, 2, 1>>(args...);
+    case 3: return launch_dsd<TileCfg<BM, 128, 2, 2, 2>>(args...);
+    case 4: return launch_dsd<TileCfg<BM, 256, 2, 2, 2>>(args...);
+    case 5: return launch_dsd<TileCfg<BM, 256, 2, 4, 1>>(args...);
+    case 6: return launch_dsd<TileCfg<BM, 256, 2, 4, 2>>(args...);
+    case 7: return launch_dsd<TileCfg<BM, 128, 2, 4, 1>>(args...);
+    case 8: return launch_dsd<TileCfg<BM, 128, 2, 4, 2>>(args...);
+    case 11: return launch_dsd_dma<DmaCfg<BM, 128, 64, 2>>(args...);
+    case 12: return launch_dsd_dma<DmaCfg<BM, 128, 64, 3>>(args...);
+    case 13: return launch_dsd_dma<DmaCfg<BM, 128, 32, 5>>(args...);
+    case 14: return launch_dsd_dma<DmaCfg<BM, 256, 64, 2>>(args...);
+    case 15: return launch_dsd_dma<DmaCfg<BM, 256, 64, 3>>(args...);
+    case 16:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 32, 6, 2, 4>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 32, 6>>(args...);
+    case 17:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 4>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 64, 3>>(args...);
+    case 18: return launch_dsd_dma<DmaCfg<BM, 128, 32, 4>>(args...);
+    case 19:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 128, 32, 5, 2, 4>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 128, 32, 5>>(args...);
+    default: return fail(SB_ERR_INVALID, "dsd: unknown tile variant %d", variant);
+  }
 }
 
 }  // namespace
@@ -150,17 +287,16 @@ extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offs
   if (!aligned16(blocks) || !aligned16(w) || !aligned16(out))
     return fail(SB_ERR_INVALID, "blocks and w must be 16-byte aligned");
   const hipStream_t s = as_stream(stream);
-  // 256-column tiles halve the re-reads of each H block; 128-column tiles
-  // when D is not a multiple of 256 or there are too few tiles to fill the GPU.
-  const bool wide = d_model % 256 == 0 && num_row_blocks * (d_model / 256) >= 4 * 256;
-  if (block_size == 128) {
-    return wide ? launch_dsd<128, 256>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks,
-                                       d_model, zero_dead_rows, s)
-                : launch_dsd<128, 128>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks,
-                                       d_model, zero_dead_rows, s);
-  }
-  return wide ? launch_dsd<64, 256>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
-                                    zero_dead_rows, s)
-              : launch_dsd<64, 128>(blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
-                                    zero_dead_rows, s);
+  const int forced = tuning_override("SPARSEBENCH_DSD_VARIANT");
+  // Default: 128-column tiles, 8 waves per workgroup on the register-staged
+  // loop (two workgroups per CU): the fastest measured on every benchmark shape.
+  int variant = forced > 0 ? forced : 7;
+  if (d_model % 256 != 0 && (variant == 2 || variant == 4 || variant == 5 || variant == 6 || variant == 14 ||
+                             variant == 15 || variant == 16 || variant == 17))
+    variant = 1;
+  if (block_size == 128)
+    return dispatch_dsd<128>(variant, blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
+                             zero_dead_rows, s);
+  return dispatch_dsd<64>(variant, blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
+                          zero_dead_rows, s);
 }

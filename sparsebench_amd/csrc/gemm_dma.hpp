@@ -1,0 +1,255 @@
+// The bf16 MFMA tile loop of SDD and DSD on gfx950, fed by LDS DMA.
+//
+// One workgroup of 4 wave64s (2 x 2) computes a BM x BN fp32 tile
+//     C[BM, BN] = A[BM, K] @ B[K, BN]
+// in K steps of 64. A has K contiguous (gathered token rows of x for SDD,
+// rows of an H block for DSD); B has N contiguous (rows of W1[e] or W2).
+//
+// Global -> LDS: buffer_load_dwordx4 ... lds. Each wave instruction writes
+// 1 KB of LDS (64 lanes x 16 bytes, consecutive) with no register staging,
+// into a STAGES-deep ring; the loads for step t+STAGES-1 are issued before
+// the MFMAs of step t and waited for with s_waitcnt vmcnt, so up to
+// STAGES-1 steps stay in flight. A lane whose buffer offset is out of range
+// gets zeros: the padding rows of SDD are filled that way, with no read.
+//
+// LDS layouts (both swizzled at 16-byte granularity, the swizzle applied by
+// choosing which global chunk each lane fetches):
+//   A  [BM][64] bf16, 128 B per row; logical chunk c of row r sits at
+//      c ^ swzA(r), swzA(r) = (r ^ r >> 3) & 7.
+//   B  [64][BN] bf16 as stored (row = k); logical chunk c of row k sits at
+//      c ^ 4 (k & 3).
+// Fragments (v_mfma_f32_32x32x16_bf16, operands swapped so that the result
+// is C transposed and each lane holds 4 consecutive output columns):
+//   W side (MFMA src A, 32 n x 16 k): two ds_read_b64_tr_b16 per block;
+//      within each 16-lane group, lane j points at row k0 + j/4, columns
+//      n0 + 4 (j % 4) .. +3, and lane i receives rows k0 .. k0+3 of column
+//      n0 + i. Groups 0/1 cover k 0-7 (two reads), groups 2/3 k 8-15.
+//   A side (MFMA src B, 16 k x 32 m): one ds_read_b128 of 8 consecutive k.
+// Both sides hold k = 8 (lane / 32) + 0..7 of the 16-step, in the same order.
+#pragma once
+
+#include "common.hpp"
+
+namespace sb {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+// Raw buffer resource word 3 for gfx9-family (CDNA) untyped loads.
+constexpr int kBufferFlags = 0x00020000;
+// Out-of-range buffer offset: loads there return zeros. Every valid offset
+// (voffset + soffset) stays below 2^31, so this never wraps into range.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(num_bytes),
+                                           kBufferFlags);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  // gfx9 encoding of s_waitcnt vmcnt(N), other counters left at their maximum.
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2>
+struct DmaCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_;
+  static constexpr int WM = WM_, WN = WN_;
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;
+  static constexpr int kARowBytes = BK * 2;
+  static constexpr int kAChunksPerRow = BK / 8;
+  static constexpr int kABytes = BM * kARowBytes;
+  static constexpr int kBRowBytes = BN * 2;
+  static constexpr int kBBytes = BK * kBRowBytes;
+  static constexpr int kStageBytes = kABytes + kBBytes;
+  static constexpr int kLdsBytes = STAGES * kStageBytes;
+  static constexpr int kAInstr = kABytes / 1024 / kWaves;  // DMA instructions per wave per step
+  static constexpr int kBInstr = kBBytes / 1024 / kWaves;
+  static constexpr int kLoadsPerStep = kAInstr + kBInstr;
+  static constexpr int kARowsPerInstr = 1024 / kARowBytes;
+  static constexpr int kBRowsPerInstr = 1024 / kBRowBytes;
+  static constexpr int kBChunksPerRow = BN / 8;
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(BN == 128 || BN == 256, "BN");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "waves own whole 32 x 32 blocks");
+  static_assert(kAInstr >= 1 && kAInstr * kWaves * 1024 == kABytes, "A step splits into whole 1 KB DMA rows");
+  static_assert(kBInstr >= 1 && kBInstr * kWaves * 1024 == kBBytes, "B step splits into whole 1 KB DMA rows");
+  static_assert(STAGES >= 2 && STAGES <= 8, "STAGES");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  static_assert(kLoadsPerStep * (STAGES - 2) <= 63, "vmcnt");
+};
+
+// A rows are BK/8 16-byte chunks: logical chunk c of row r sits at c ^ swz_a(r).
+// 16 consecutive rows read at one logical chunk hit 16 different 16-byte bank
+// groups of the 256-byte bank span.
+template <int BK>
+__device__ __forceinline__ int swz_a(int r) {
+  if constexpr (BK == 64) return (r ^ (r >> 3)) & 7;  // 2 rows per 256 B
+  else return (r >> 2) & 3;                             // 4 rows per 256 B
+}
+
+// This lane's LDS row / chunk for A DMA instruction q, and the logical
+// chunk it must fetch.
+template <class Cfg>
+struct ADmaPos {
+  int row[Cfg::kAInstr];
+  int chunk[Cfg::kAInstr];  // logical 16-byte chunk (8 k values)
+  __device__ __forceinline__ ADmaPos() {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < Cfg::kAInstr; ++q) {
+      row[q] = Cfg::kARowsPerInstr * (Cfg::kAInstr * wave + q) + lane / Cfg::kAChunksPerRow;
+      chunk[q] = (lane % Cfg::kAChunksPerRow) ^ swz_a<Cfg::BK>(row[q]);
+    }
+  }
+};
+
+template <class Cfg>
+struct BDmaPos {
+  int row[Cfg::kBInstr];    // k row within the step
+  int col[Cfg::kBInstr];    // first of 8 n columns (logical)
+  __device__ __forceinline__ BDmaPos() {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < Cfg::kBInstr; ++q) {
+      row[q] = Cfg::kBRowsPerInstr * (Cfg::kBInstr * wave + q) + lane / Cfg::kBChunksPerRow;
+      const int p = lane % Cfg::kBChunksPerRow;
+      col[q] = 8 * (p ^ (4 * (row[q] & 3)));
+    }
+  }
+};
+
+// s_waitcnt vmcnt(later * L) for a run-time `later` in [0, MAXL].
+template <int L, int MAXL>
+__device__ __forceinline__ void wait_steps(int later) {
+  if constexpr (MAXL <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (later >= MAXL) wait_vmcnt<MAXL * L>();
+    else wait_steps<L, MAXL - 1>(later);
+  }
+}
+
+// Per-step sources, supplied by the kernel:
+//   a_src(t, &rsrc, &soffset), b_src(t, &rsrc, &soffset)
+// and fixed per-lane offsets a_voff[kAInstr], b_voff[kBInstr] (bytes).
+template <class Cfg>
+struct DmaMainloop {
+  using Acc = f32x16_t[Cfg::TN][Cfg::TM];  // acc[j][i]: C^T block (n block j, m block i)
+
+  template <class Src>
+  __device__ __forceinline__ static void issue(uint8_t* lds, int t, const Src& src) {
+    const int wave = threadIdx.x >> 6;
+    uint8_t* stage = lds + (t % Cfg::STAGES) * Cfg::kStageBytes;
+    __amdgpu_buffer_rsrc_t ra, rb;
+    uint32_t sa, sb;
+    src.a_src(t, &ra, &sa);
+    src.b_src(t, &rb, &sb);
+#pragma unroll
+    for (int q = 0; q < Cfg::kAInstr; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024), 16,
+                                               src.a_voff[q], sa, 0, 0);
+#pragma unroll
+    for (int q = 0; q < Cfg::kBInstr; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q) * 1024), 16, src.b_voff[q], sb, 0, 0);
+  }
+
+  __device__ __forceinline__ static void compute(const uint8_t* stage, Acc& acc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+    const int h = lane >> 5;
+    const uint8_t* as = stage;
+    const uint8_t* bs = stage + Cfg::kABytes;
+    // A side: row m = wm*WTM + 32 i + lane % 32.
+    int a_row_off[Cfg::TM], a_swz[Cfg::TM];
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; ++i) {
+      const int r = wm * Cfg::WTM + 32 * i + (lane & 31);
+      a_row_off[i] = r * Cfg::kARowBytes;
+      a_swz[i] = swz_a<Cfg::BK>(r);
+    }
+    // W side: lane j of its 16-group reads row (k0 + j/4), columns
+    // n0 + 16 (group % 2) + 4 (j % 4); chunk block (4 chunks = 64 B) of
+    // n block jn is XORed with (k & 3) = j / 4.
+    const int g = lane >> 4, jj = lane & 15;
+    const int krow = 8 * (g >> 1) + (jj >> 2);
+    int b_off[Cfg::TN];
+#pragma unroll
+    for (int jn = 0; jn < Cfg::TN; ++jn) {
+      const int blk = (wn * Cfg::WTN) / 32 + jn;                // 32-column block index
+      const int chunk = 4 * (blk ^ (jj >> 2)) + 2 * (g & 1) + ((jj & 3) >> 1);
+      b_off[jn] = krow * Cfg::kBRowBytes + chunk * 16 + (jj & 1) * 8;
+    }
+#pragma unroll
+    for (int s = 0; s < Cfg::BK / 16; ++s) {
+      bf16x8_t a[Cfg::TM];
+#pragma unroll
+      for (int i = 0; i < Cfg::TM; ++i)
+        a[i] = *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * s + h) ^ a_swz[i]) << 4));
+      bf16x8_t b[Cfg::TN];
+#pragma unroll
+      for (int jn = 0; jn < Cfg::TN; ++jn) {
+        const uint8_t* p = bs + b_off[jn] + 16 * s * Cfg::kBRowBytes;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * Cfg::kBRowBytes));
+        b[jn] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int jn = 0; jn < Cfg::TN; ++jn)
+#pragma unroll
+        for (int i = 0; i < Cfg::TM; ++i)
+          acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[jn], a[i], acc[jn][i], 0, 0, 0);
+    }
+  }
+
+  template <class Src>
+  __device__ __forceinline__ static void run(uint8_t* lds, const Src& src, int num_steps, Acc& acc) {
+#pragma unroll
+    for (int jn = 0; jn < Cfg::TN; ++jn)
+#pragma unroll
+      for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[jn][i][v] = 0.0f;
+    if (num_steps <= 0) return;
+#pragma unroll
+    for (int s = 0; s < Cfg::STAGES - 1; ++s)
+      if (s < num_steps) issue(lds, s, src);
+    for (int t = 0; t < num_steps; ++t) {
+      // Step t's loads are complete once at most the later issued steps
+      // (t+1 .. t+STAGES-2, if they exist) are outstanding.
+      wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(min(num_steps - 1 - t, Cfg::STAGES - 2));
+      // Every wave's step-t data is in LDS, and every wave is done with
+      // step t-1's stage, which the next issue overwrites.
+      __builtin_amdgcn_s_barrier();
+      if (t + Cfg::STAGES - 1 < num_steps) issue(lds, t + Cfg::STAGES - 1, src);
+      compute(lds + (t % Cfg::STAGES) * Cfg::kStageBytes, acc);
+    }
+  }
+
+  // Output coordinates of acc[jn][i][v] for this lane: the MFMA computed C^T,
+  // so lane % 32 is the C row and v selects the column:
+  //   m = wm*WTM + 32 i + lane % 32
+  //   n = wn*WTN + 32 jn + 8 (v / 4) + 4 (lane / 32) + v % 4
+  // Values v = 4g .. 4g+3 are four consecutive columns.
+  __device__ __forceinline__ static int out_row(int i) {
+    const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) / Cfg::WN;
+    return wm * Cfg::WTM + 32 * i + (lane & 31);
+  }
+  __device__ __forceinline__ static int out_col(int jn, int g) {
+    const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) % Cfg::WN;
+    return wn * Cfg::WTN + 32 * jn + 8 * g + 4 * (lane >> 5);
+  }
+};
+
+}  // namespace sb

@@ -16,6 +16,7 @@
 
 #include <type_traits>
 
+#include "gemm_dma.hpp"
 #include "gemm_tile.hpp"
 
 namespace sb {
@@ -23,7 +24,25 @@ namespace {
 
 constexpr int kBS = 128;
 
-__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f)); }
+// Exact-erf GELU, 0.5 v (1 + erf(v / sqrt 2)), in fp32.
+//
+// erfc(u) for u >= 0 by Abramowitz & Stegun 7.1.26 (Hastings' rational
+// approximation, |error| <= 1.5e-7): erfc(u) = t P(t) exp(-u^2),
+// t = 1 / (1 + p u). Branch-free, about fifteen instructions, and for
+// v < 0 it forms 1 - erf(u) = erfc(u) directly, with no cancellation.
+__device__ __forceinline__ float gelu_erf_fast(float v) {
+  const float u = fabsf(v) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, u, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  const float erfc_u = poly * t * __builtin_amdgcn_exp2f(-u * u * 1.44269504088896341f);
+  return v >= 0.0f ? v * (1.0f - 0.5f * erfc_u) : 0.5f * v * erfc_u;
+}
+
+// The same with the device library's erff (reference accuracy, slower).
+__device__ __forceinline__ float gelu_erf_libm(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f)); }
 
 template <class Cfg>
 struct SddLoader {
@@ -53,20 +72,22 @@ struct SddLoader {
   }
 };
 
-template <int BN>
-__global__ void __launch_bounds__(256)
+template <class Cfg, bool kFastGelu>
+__global__ void __launch_bounds__(Cfg::kThreads)
     sdd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1, const int32_t* __restrict__ row_token,
                const int32_t* __restrict__ row_block_expert, const int32_t* __restrict__ row_offsets,
                uint16_t* __restrict__ out, int32_t num_tokens, int32_t d_model, int32_t ffn_dim, int32_t num_experts,
-               int32_t num_row_blocks, int32_t num_slices, int32_t apply_gelu) {
-  using Cfg = TileCfg<kBS, BN>;
+               int32_t num_row_blocks, int32_t num_slices, int32_t apply_gelu, int32_t group) {
   using ML = Mainloop<Cfg>;
+  constexpr int BN = Cfg::BN;
+  static_assert(Cfg::BM == kBS, "one row block per tile");
   __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::kLdsElems];
 
-  const int live = live_row_blocks(row_offsets, num_row_blocks) * num_slices;
-  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live);
-  const int rb = tile / num_slices;
-  const int n0 = (tile % num_slices) * BN;
+  const int live_rb = live_row_blocks(row_offsets, num_row_blocks);
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
+  int rb, slice;
+  tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
+  const int n0 = slice * BN;
   const int32_t begin = row_offsets[rb];
   const int32_t end = row_offsets[rb + 1];
   const int32_t ffn_blocks = ffn_dim / kBS;
@@ -104,24 +125,151 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         float h = acc[i][j][v];
-        if (apply_gelu) h = gelu_erf(h);
+        if (apply_gelu) h = kFastGelu ? gelu_erf_fast(h) : gelu_erf_libm(h);
         col[ML::acc_row(i, v) * kBS] = f32_to_bf16(h);
       }
   }
 }
 
-template <int BN>
-int launch_sdd(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
-               const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
-               int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, hipStream_t stream) {
-  const int32_t num_slices = static_cast<int32_t>(ffn_dim / BN);
+// The same tile on the LDS-DMA mainloop (gemm_dma.hpp): token rows are
+// gathered by the buffer loads themselves, padding rows read out of range
+// and land in LDS as zeros.
+template <class Cfg>
+struct SddDmaSrc {
+  __amdgpu_buffer_rsrc_t x_rsrc, w_rsrc;
+  uint32_t a_voff[Cfg::kAInstr];
+  uint32_t b_voff[Cfg::kBInstr];
+  uint32_t b_step_bytes;
+  __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    *r = x_rsrc;
+    *s = static_cast<uint32_t>(t) * (Cfg::BK * 2);
+  }
+  __device__ __forceinline__ void b_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    *r = w_rsrc;
+    *s = static_cast<uint32_t>(t) * b_step_bytes;
+  }
+};
+
+template <class Cfg, bool kFastGelu>
+__global__ void __launch_bounds__(Cfg::kThreads)
+    sdd_dma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
+                   const int32_t* __restrict__ row_token, const int32_t* __restrict__ row_block_expert,
+                   const int32_t* __restrict__ row_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
+                   int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t num_row_blocks, int32_t num_slices,
+                   int32_t apply_gelu, int32_t group) {
+  using ML = DmaMainloop<Cfg>;
+  constexpr int BN = Cfg::BN;
+  static_assert(Cfg::BM == kBS, "one row block per tile");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+
+  const int live_rb = live_row_blocks(row_offsets, num_row_blocks);
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
+  int rb, slice;
+  tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
+  const int n0 = slice * BN;
+  const int32_t begin = row_offsets[rb];
+  const int32_t end = row_offsets[rb + 1];
+  const int32_t ffn_blocks = ffn_dim / kBS;
+  if (begin == end) return;
+  const int32_t expert = row_block_expert[rb];
+  if (end - begin != ffn_blocks || begin < 0 || end > num_row_blocks * ffn_blocks || expert < 0 ||
+      expert >= num_experts)
+    return;
+
+  SddDmaSrc<Cfg> src;
+  src.x_rsrc = make_rsrc(x, static_cast<uint32_t>(num_tokens) * static_cast<uint32_t>(d_model) * 2u);
+  src.w_rsrc = make_rsrc(w1 + static_cast<int64_t>(expert) * d_model * ffn_dim,
+                         static_cast<uint32_t>(d_model) * static_cast<uint32_t>(ffn_dim) * 2u);
+  src.b_step_bytes = static_cast<uint32_t>(Cfg::BK) * static_cast<uint32_t>(ffn_dim) * 2u;
+  const ADmaPos<Cfg> ap;
+#pragma unroll
+  for (int q = 0; q < Cfg::kAInstr; ++q) {
+    const int32_t tok = row_token[static_cast<int64_t>(rb) * kBS + ap.row[q]];
+    src.a_voff[q] = (tok >= 0 && tok < num_tokens)
+                        ? static_cast<uint32_t>(tok) * static_cast<uint32_t>(d_model) * 2u + ap.chunk[q] * 16u
+                        : kOutOfRange;
+  }
+  const BDmaPos<Cfg> bp;
+#pragma unroll
+  for (int q = 0; q < Cfg::kBInstr; ++q)
+    src.b_voff[q] = (static_cast<uint32_t>(bp.row[q]) * ffn_dim + n0 + bp.col[q]) * 2u;
+
+  typename ML::Acc acc;
+  ML::run(lds, src, d_model / Cfg::BK, acc);
+
+  // C[m, f] -> block begin + f/128, row m, column f % 128; 4 columns per store.
+  uint16_t* blocks = out + static_cast<int64_t>(begin) * kBS * kBS;
+#pragma unroll
+  for (int jn = 0; jn < Cfg::TN; ++jn)
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; ++i) {
+      const int m = ML::out_row(i);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int f = n0 + ML::out_col(jn, g);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[jn][i][4 * g + e];
+          if (apply_gelu) v[e] = kFastGelu ? gelu_erf_fast(v[e]) : gelu_erf_libm(v[e]);
+        }
+        *reinterpret_cast<u32x2_t*>(blocks + static_cast<int64_t>(f / kBS) * kBS * kBS + m * kBS + (f % kBS)) =
+            u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      }
+    }
+}
+
+template <class Cfg, bool kFastGelu>
+int launch_sdd_dma(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+                   const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
+                   int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, hipStream_t stream) {
+  const int32_t num_slices = static_cast<int32_t>(ffn_dim / Cfg::BN);
   const int64_t tiles = num_row_blocks * num_slices;
-  sdd_kernel<BN><<<static_cast<uint32_t>(tiles), 256, 0, stream>>>(
+  sdd_dma_kernel<Cfg, kFastGelu><<<static_cast<uint32_t>(tiles), Cfg::kThreads, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
       static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens), static_cast<int32_t>(d_model),
       static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts), static_cast<int32_t>(num_row_blocks),
-      num_slices, apply_gelu);
+      num_slices, apply_gelu, tile_group());
   return check_launch("sdd");
+}
+
+template <class Cfg, bool kFastGelu>
+int launch_sdd(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+               const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
+               int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, hipStream_t stream) {
+  const int32_t num_slices = static_cast<int32_t>(ffn_dim / Cfg::BN);
+  const int64_t tiles = num_row_blocks * num_slices;
+  sdd_kernel<Cfg, kFastGelu><<<static_cast<uint32_t>(tiles), Cfg::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
+      static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens), static_cast<int32_t>(d_model),
+      static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts), static_cast<int32_t>(num_row_blocks),
+      num_slices, apply_gelu, tile_group());
+  return check_launch("sdd");
+}
+
+// Tile variants (BM x BN, waves WM x WN, register prefetch depth). 0 = pick by shape.
+template <bool kFastGelu, class... Args>
+int dispatch_sdd(int variant, Args... args) {
+  switch (variant) {
+    case 1: return launch_sdd<TileCfg<128, 128, 2, 2, 1>, kFastGelu>(args...);
+    case 2: return launch_sdd<TileCfg<128, 256, 2, 2, 1>, kFastGelu>(args...);
+    case 3: return launch_sdd<TileCfg<128, 128, 2, 2, 2>, kFastGelu>(args...);
+    case 4: return launch_sdd<TileCfg<128, 256, 2, 2, 2>, kFastGelu>(args...);
+    case 5: return launch_sdd<TileCfg<128, 256, 2, 4, 1>, kFastGelu>(args...);
+    case 6: return launch_sdd<TileCfg<128, 256, 2, 4, 2>, kFastGelu>(args...);
+    case 7: return launch_sdd<TileCfg<128, 128, 2, 4, 1>, kFastGelu>(args...);
+    case 8: return launch_sdd<TileCfg<128, 128, 2, 4, 2>, kFastGelu>(args...);
+    case 11: return launch_sdd_dma<DmaCfg<128, 128, 64, 2>, kFastGelu>(args...);
+    case 12: return launch_sdd_dma<DmaCfg<128, 128, 64, 3>, kFastGelu>(args...);
+    case 13: return launch_sdd_dma<DmaCfg<128, 128, 32, 5>, kFastGelu>(args...);
+    case 14: return launch_sdd_dma<DmaCfg<128, 256, 64, 2>, kFastGelu>(args...);
+    case 15: return launch_sdd_dma<DmaCfg<128, 256, 64, 3>, kFastGelu>(args...);
+    case 16: return launch_sdd_dma<DmaCfg<128, 256, 32, 6, 2, 4>, kFastGelu>(args...);
+    case 17: return launch_sdd_dma<DmaCfg<128, 256, 64, 3, 2, 4>, kFastGelu>(args...);
+    case 18: return launch_sdd_dma<DmaCfg<128, 128, 32, 4>, kFastGelu>(args...);
+    case 19: return launch_sdd_dma<DmaCfg<128, 128, 32, 5, 2, 4>, kFastGelu>(args...);
+    default: return fail(SB_ERR_INVALID, "sdd: unknown tile variant %d", variant);
+  }
 }
 
 }  // namespace
@@ -145,16 +293,21 @@ extern "C" int sb_sdd(const void* x, const void* w1, const int32_t* row_token, c
     return fail(SB_ERR_INVALID, "sdd needs F (%lld) to be a multiple of 256", static_cast<long long>(ffn_dim));
   if (num_tokens <= 0 || num_tokens > kI32Max || num_experts <= 0 || num_experts > kI32Max)
     return fail(SB_ERR_INVALID, "sdd: bad token or expert count");
+  // Buffer offsets are 32-bit: x and one expert's W1 must each stay under 2 GB.
+  if (num_tokens * d_model * 2 >= (int64_t{1} << 31) - 2 * d_model)
+    return fail(SB_ERR_INVALID, "sdd: x too large for 32-bit buffer offsets");
   if (num_row_blocks * (ffn_dim / 128) > kI32Max || ffn_dim * d_model > kI32Max ||
       num_tokens * d_model > (int64_t{1} << 62) || num_row_blocks * 128 > kI32Max)
     return fail(SB_ERR_INVALID, "problem too large");
   const hipStream_t s = as_stream(stream);
-  // 256-column tiles read each gathered A tile half as often; 128-column
-  // tiles double the workgroup count when there are too few row blocks to
-  // fill 256 CUs a few times over.
-  if (num_row_blocks * (ffn_dim / 256) >= 4 * 256)
-    return launch_sdd<256>(x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model, ffn_dim,
-                           num_experts, num_row_blocks, apply_gelu, s);
-  return launch_sdd<128>(x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model, ffn_dim,
-                         num_experts, num_row_blocks, apply_gelu, s);
+  const int forced = tuning_override("SPARSEBENCH_SDD_VARIANT");
+  const int gelu_mode = tuning_override("SPARSEBENCH_GELU_LIBM");
+  // Default: 128 x 128 tiles on the LDS-DMA loop, two stages (64 KB LDS, two
+  // workgroups per CU): the fastest measured on every benchmark shape.
+  const int variant = forced > 0 ? forced : 11;
+  if (gelu_mode > 0)
+    return dispatch_sdd<false>(variant, x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model,
+                               ffn_dim, num_experts, num_row_blocks, apply_gelu, s);
+  return dispatch_sdd<true>(variant, x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model,
+                            ffn_dim, num_experts, num_row_blocks, apply_gelu, s);
 }

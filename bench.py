@@ -51,6 +51,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-stages", action="store_true", help="skip the eager per-stage breakdown")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only copy 1 GiB five times (torch's copy kernel): the reference point that scales "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     p.add_argument("--kernel-loop", type=int, default=0,
                    help="after the bench, replay the graph N more times (for rocprofv3 runs)")
     return p.parse_args()
@@ -77,6 +80,21 @@ def algorithmic_bytes(shape, active_experts: int) -> dict[str, int]:
         "dsd": n * f * 2 + active_experts * f * d * 2 + n * d * 2,
         "combine": n * d * 2 + n * (2 + 4) + t * d * 2,
     }
+
+
+def measured_traffic(config: str, routing: str, stage: str) -> int | None:
+    """HBM bytes per launch of `stage` from the committed rocprofv3 FETCH/WRITE summary, if one exists."""
+    import pathlib
+    import re
+
+    for path in sorted(pathlib.Path(__file__).resolve().parent.glob("profiles/traffic_*.md")):
+        for line in path.read_text().splitlines():
+            m = re.match(r"\s*traffic_bytes (\S+) (\S+) (.*)", line)
+            if m and m.group(1) == config and m.group(2) == routing:
+                values = dict(kv.split("=") for kv in m.group(3).split())
+                if stage in values:
+                    return int(values[stage])
+    return None
 
 
 def cpu_baseline(shape, routing: str, seed: int) -> dict:
@@ -141,6 +159,14 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (MI355X)", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("copied 1 GiB x 5")
+        return 0
 
     from sparsebench_amd.moe import moe_forward
     from sparsebench_amd.workloads import SHAPES, make_layer
@@ -243,13 +269,15 @@ def main() -> int:
         if hbm_bound:
             achieved = nbytes[name] / (kms * 1e-3) / 1e9
             roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": f"{name} stage (one kernel)",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic(args.config, args.routing, name), "kernel": f"{name} stage (one kernel)",
                         "algorithmic_bytes": nbytes[name], "kernel_ms": kms,
                         "useful_tflops": round(flops / (kms * 1e-3) / 1e12, 2)}
         else:
             achieved = flops / (kms * 1e-3) / 1e12
             roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                        "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                        "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "traffic": measured_traffic(args.config, args.routing, name),
                         "kernel": f"{name} stage (one kernel)", "useful_flops": flops, "kernel_ms": kms}
 
     cpu = None

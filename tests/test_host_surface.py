@@ -1,0 +1,88 @@
+"""Host-side surface on the CPU: the drop-in module aliasing of INTEGRATION.md,
+the reference-shaped dataclasses, and argument errors raised before any GPU call."""
+
+import dataclasses
+import sys
+
+import pytest
+import torch
+
+
+def test_package_aliases_as_sparsebench() -> None:
+    import sparsebench_amd
+    from sparsebench_amd import _C, moe, routing, spmm, topology, workloads
+
+    saved = {k: v for k, v in sys.modules.items() if k == "sparsebench" or k.startswith("sparsebench.")}
+    try:
+        for name, mod in {"": sparsebench_amd, "._C": _C, ".moe": moe, ".routing": routing, ".spmm": spmm,
+                          ".topology": topology, ".workloads": workloads}.items():
+            sys.modules["sparsebench" + name] = mod
+        from sparsebench.moe import moe_forward  # noqa: F401  (the reference's import line)
+        from sparsebench.routing import DeviceTopology, route_device  # noqa: F401
+        from sparsebench import _C as c
+
+        assert {"arch_probe", "build_topology_cuda", "sdd_cuda", "dsd_cuda"} <= set(dir(c))
+    finally:
+        for k in [k for k in sys.modules if k == "sparsebench" or k.startswith("sparsebench.")]:
+            del sys.modules[k]
+        sys.modules.update(saved)
+
+
+def test_topology_fields_match_the_reference_order() -> None:
+    from sparsebench_amd.routing import DeviceTopology
+    from sparsebench_amd.topology import Topology
+
+    common = ["block_size", "num_experts", "ffn_blocks", "tokens_per_expert", "padded_offsets", "row_token",
+              "copy_row", "row_block_expert", "row_offsets", "col_indices"]
+    assert [f.name for f in dataclasses.fields(Topology)] == common
+    assert [f.name for f in dataclasses.fields(DeviceTopology)] == common + ["error"]
+
+
+def test_build_topology_rejects_cpu_tensor() -> None:
+    from sparsebench_amd.routing import build_topology_cuda
+
+    with pytest.raises(RuntimeError, match="CUDA"):
+        build_topology_cuda(torch.tensor([[0, 1]]), 8, 32, 16)
+
+
+def test_dsd_rejects_cpu_weights() -> None:
+    from sparsebench_amd import _C
+
+    with pytest.raises(RuntimeError, match="CUDA"):
+        _C.dsd_cuda(torch.zeros(1, 64, 64, dtype=torch.bfloat16), torch.zeros(64, 128, dtype=torch.bfloat16),
+                    torch.zeros(2, dtype=torch.int32), torch.zeros(1, dtype=torch.int32), 1)
+
+
+def test_sdd_wrapper_rejects_block_size_64_before_the_gpu() -> None:
+    from sparsebench_amd.spmm import sdd
+    from sparsebench_amd.topology import Topology
+
+    z = torch.zeros(1, dtype=torch.int32)
+    topo = Topology(64, 4, 4, z, z, z, z, z, z, z)
+    with pytest.raises(ValueError, match="block size 128"):
+        sdd(torch.zeros(2, 64, dtype=torch.bfloat16), torch.zeros(4, 64, 256, dtype=torch.bfloat16), topo)
+
+
+def test_moe_forward_rejects_mismatched_shapes_before_the_gpu() -> None:
+    from sparsebench_amd.moe import moe_forward
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w1 = torch.zeros(2, 64, 256, dtype=torch.bfloat16)
+    idx = torch.zeros(4, 2, dtype=torch.long)
+    with pytest.raises(ValueError, match="w2"):
+        moe_forward(x, idx, torch.ones(4, 2), w1, torch.zeros(2, 64, 256, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="x must be"):
+        moe_forward(x, idx, torch.ones(4, 1), w1, torch.zeros(2, 256, 64, dtype=torch.bfloat16))
+
+
+def test_workload_shapes_and_flops() -> None:
+    from sparsebench_amd.workloads import SHAPES, routing_case
+
+    fg = SHAPES["fine_grained"]
+    assert fg.useful_flops == 2 * 2 * 4096 * 2 * 1024 * 4096  # 137.44 GFLOP, as the reference counts it
+    idx = routing_case("zipf_perm", 4096, 64, seed=0)
+    assert idx.shape == (4096, 2) and bool((idx[:, 0] != idx[:, 1]).all())
+    assert torch.equal(idx, routing_case("zipf_perm", 4096, 64, seed=0))
+    # Zipf over a permutation: the hottest expert is not expert 0 for this seed, and counts are skewed.
+    counts = torch.bincount(idx.flatten(), minlength=64)
+    assert int(counts.max()) > 4 * int(counts.float().median())

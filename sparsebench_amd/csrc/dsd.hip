@@ -58,7 +58,7 @@ struct DsdLoader {
     }
     const uint16_t* src = w_cols + (row0 + kin + pos.b_kgroup * 8) * d_model + pos.b_col;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) b[r] = *reinterpret_cast<const BRow*>(src + r * d_model);
+    for (int r = 0; r < 8; ++r) b[r] = load_vec<Cfg::NTB, BRow>(src + r * d_model);
   }
 };
 
@@ -258,6 +258,27 @@ int dispatch_dsd(int variant, Args... args) {
     case 19:
       if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 128, 32, 5, 2, 4>>(args...);
       else return launch_dsd_dma<DmaCfg<BM, 128, 32, 5>>(args...);
+    case 9: return launch_dsd<TileCfg<BM, 128, 2, 4, 1, true>>(args...);
+    case 10: return launch_dsd<TileCfg<BM, 128, 2, 2, 1, true>>(args...);
+    case 21: return launch_dsd_dma<DmaCfg<BM, 128, 64, 2, 2, 2, 0, 2>>(args...);
+    case 22: return launch_dsd_dma<DmaCfg<BM, 128, 64, 2, 2, 2, 2, 2>>(args...);
+    case 23: return launch_dsd_dma<DmaCfg<BM, 128, 64, 3, 2, 2, 0, 2>>(args...);
+    case 24: return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 2, 0, 2>>(args...);
+    case 25:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 4, 0, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 2, 0, 2>>(args...);
+    case 26: return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 2, 0, 2>>(args...);
+    case 27: return launch_dsd_dma<DmaCfg<BM, 128, 32, 5, 2, 2, 0, 2>>(args...);
+    case 31: return launch_dsd_dma<DmaCfg<BM, 512, 64, 2, 1, 4, 0, 2>>(args...);
+    case 32: return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2>>(args...);
+    case 33: return launch_dsd_dma<DmaCfg<BM, 512, 32, 3, 1, 4, 0, 2>>(args...);
+    case 34:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 32, 3, 2, 4, 0, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 32, 3, 2, 2, 0, 2>>(args...);
+    case 35: return launch_dsd_dma<DmaCfg<BM, 256, 32, 3, 2, 2, 0, 2>>(args...);
+    case 36:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 4, 0, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 2, 0, 2>>(args...);
     default: return fail(SB_ERR_INVALID, "dsd: unknown tile variant %d", variant);
   }
 }
@@ -288,12 +309,18 @@ extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offs
     return fail(SB_ERR_INVALID, "blocks and w must be 16-byte aligned");
   const hipStream_t s = as_stream(stream);
   const int forced = tuning_override("SPARSEBENCH_DSD_VARIANT");
-  // Default: 128-column tiles, 8 waves per workgroup on the register-staged
-  // loop (two workgroups per CU): the fastest measured on every benchmark shape.
-  int variant = forced > 0 ? forced : 7;
+  // Default, from timing every variant on the benchmark shapes (MI355X):
+  // 128 x 512 tiles, 4 waves, BK 32 x 4-stage LDS-DMA ring with non-temporal
+  // W loads. With a deep reduction (row K = F per expert >= 8192, read from
+  // the buffer shape: nnz / num_row_blocks blocks per row) there are enough
+  // K steps per tile that 128 x 128 tiles balance the CUs better.
+  const int64_t row_k = num_row_blocks > 0 ? nnz / num_row_blocks * block_size : 0;
+  int variant = forced > 0 ? forced : (row_k >= 8192 ? 11 : 32);
   if (d_model % 256 != 0 && (variant == 2 || variant == 4 || variant == 5 || variant == 6 || variant == 14 ||
-                             variant == 15 || variant == 16 || variant == 17))
+                             variant == 15 || variant == 16 || variant == 17 || variant == 24 || variant == 25 ||
+                             variant == 26 || variant == 34 || variant == 35 || variant == 36))
     variant = 1;
+  if (d_model % 512 != 0 && variant >= 31 && variant <= 33) variant = d_model % 256 == 0 ? 25 : 21;
   if (block_size == 128)
     return dispatch_dsd<128>(variant, blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
                              zero_dead_rows, s);

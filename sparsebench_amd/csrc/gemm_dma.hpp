@@ -58,9 +58,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2>
+// CPA / CPB: cache policy of the A / B loads (buffer instruction bits; 2 = nt,
+// a streaming hint that keeps the read-once weight stream from displacing
+// reusable lines).
+template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0>
 struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_;
+  static constexpr int CPA = CPA_, CPB = CPB_;
   static constexpr int WM = WM_, WN = WN_;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
@@ -77,10 +81,11 @@ struct DmaCfg {
   static constexpr int kBInstr = kBBytes / 1024 / kWaves;
   static constexpr int kLoadsPerStep = kAInstr + kBInstr;
   static constexpr int kARowsPerInstr = 1024 / kARowBytes;
-  static constexpr int kBRowsPerInstr = 1024 / kBRowBytes;
+  static constexpr int kBRowsPerInstr = kBRowBytes >= 1024 ? 1 : 1024 / kBRowBytes;
+  static_assert(kBRowBytes <= 1024, "one DMA row per instruction at most");
   static constexpr int kBChunksPerRow = BN / 8;
   static_assert(BK == 32 || BK == 64, "BK");
-  static_assert(BN == 128 || BN == 256, "BN");
+  static_assert(BN == 128 || BN == 256 || BN == 512, "BN");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "waves own whole 32 x 32 blocks");
   static_assert(kAInstr >= 1 && kAInstr * kWaves * 1024 == kABytes, "A step splits into whole 1 KB DMA rows");
   static_assert(kBInstr >= 1 && kBInstr * kWaves * 1024 == kBBytes, "B step splits into whole 1 KB DMA rows");
@@ -147,8 +152,12 @@ template <class Cfg>
 struct DmaMainloop {
   using Acc = f32x16_t[Cfg::TN][Cfg::TM];  // acc[j][i]: C^T block (n block j, m block i)
 
+  // issue() and compute() take their LDS stage through __restrict__ pointers:
+  // the DMA of step t+STAGES-1 writes a different stage than the one step t
+  // reads, and saying so lets the compiler drop the vmcnt(0) it would
+  // otherwise put before every LDS read (which serializes loads and MFMAs).
   template <class Src>
-  __device__ __forceinline__ static void issue(uint8_t* lds, int t, const Src& src) {
+  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int t, const Src& src) {
     const int wave = threadIdx.x >> 6;
     uint8_t* stage = lds + (t % Cfg::STAGES) * Cfg::kStageBytes;
     __amdgpu_buffer_rsrc_t ra, rb;
@@ -158,14 +167,14 @@ struct DmaMainloop {
 #pragma unroll
     for (int q = 0; q < Cfg::kAInstr; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024), 16,
-                                               src.a_voff[q], sa, 0, 0);
+                                               src.a_voff[q], sa, 0, Cfg::CPA);
 #pragma unroll
     for (int q = 0; q < Cfg::kBInstr; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q) * 1024), 16, src.b_voff[q], sb, 0, 0);
+          rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q) * 1024), 16, src.b_voff[q], sb, 0, Cfg::CPB);
   }
 
-  __device__ __forceinline__ static void compute(const uint8_t* stage, Acc& acc) {
+  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ stage, Acc& acc) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     const int h = lane >> 5;

@@ -45,8 +45,10 @@ struct BRowOf<4> { using type = u32x2_t; };
 template <>
 struct BRowOf<2> { using type = u32x1_t; };
 
-template <int BM_, int BN_, int WM_ = 2, int WN_ = 2, int PF_ = 1>
+// NTB: load B (the weights) with the non-temporal hint.
+template <int BM_, int BN_, int WM_ = 2, int WN_ = 2, int PF_ = 1, bool NTB_ = false>
 struct TileCfg {
+  static constexpr bool NTB = NTB_;
   static constexpr int BM = BM_;
   static constexpr int BN = BN_;
   static constexpr int BK = 64;
@@ -68,6 +70,14 @@ struct TileCfg {
   static_assert(PF == 1 || PF == 2, "prefetch depth 1 or 2");
   using BRow = typename BRowOf<kBCols>::type;
 };
+
+// 8- or 16-byte global load, optionally with the non-temporal hint.
+template <bool NT, class V>
+__device__ __forceinline__ V load_vec(const uint16_t* p) {
+  const V* q = reinterpret_cast<const V*>(p);
+  if constexpr (NT) return __builtin_nontemporal_load(q);
+  else return *q;
+}
 
 // Chunk position of logical chunk c in LDS row r.
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }

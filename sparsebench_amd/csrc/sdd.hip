@@ -68,7 +68,7 @@ struct SddLoader {
   __device__ __forceinline__ void load_b(int t, const typename ML::LoadPos& p, BRow (&b)[8]) const {
     const uint16_t* src = w_cols + (static_cast<int64_t>(t) * Cfg::BK + p.b_kgroup * 8) * ffn_dim + p.b_col;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) b[r] = *reinterpret_cast<const BRow*>(src + r * ffn_dim);
+    for (int r = 0; r < 8; ++r) b[r] = load_vec<Cfg::NTB, BRow>(src + r * ffn_dim);
   }
 };
 
@@ -223,6 +223,7 @@ template <class Cfg, bool kFastGelu>
 int launch_sdd_dma(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
                    const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
                    int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, hipStream_t stream) {
+  if (ffn_dim % Cfg::BN != 0) return fail(SB_ERR_INVALID, "sdd: F %% tile width != 0");
   const int32_t num_slices = static_cast<int32_t>(ffn_dim / Cfg::BN);
   const int64_t tiles = num_row_blocks * num_slices;
   sdd_dma_kernel<Cfg, kFastGelu><<<static_cast<uint32_t>(tiles), Cfg::kThreads, 0, stream>>>(
@@ -268,6 +269,21 @@ int dispatch_sdd(int variant, Args... args) {
     case 17: return launch_sdd_dma<DmaCfg<128, 256, 64, 3, 2, 4>, kFastGelu>(args...);
     case 18: return launch_sdd_dma<DmaCfg<128, 128, 32, 4>, kFastGelu>(args...);
     case 19: return launch_sdd_dma<DmaCfg<128, 128, 32, 5, 2, 4>, kFastGelu>(args...);
+    case 9: return launch_sdd<TileCfg<128, 128, 2, 4, 1, true>, kFastGelu>(args...);
+    case 10: return launch_sdd<TileCfg<128, 128, 2, 2, 1, true>, kFastGelu>(args...);
+    case 21: return launch_sdd_dma<DmaCfg<128, 128, 64, 2, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 22: return launch_sdd_dma<DmaCfg<128, 128, 64, 2, 2, 2, 2, 2>, kFastGelu>(args...);
+    case 23: return launch_sdd_dma<DmaCfg<128, 128, 64, 3, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 24: return launch_sdd_dma<DmaCfg<128, 256, 64, 2, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 25: return launch_sdd_dma<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2>, kFastGelu>(args...);
+    case 26: return launch_sdd_dma<DmaCfg<128, 256, 64, 3, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 27: return launch_sdd_dma<DmaCfg<128, 128, 32, 5, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 31: return launch_sdd_dma<DmaCfg<128, 512, 64, 2, 1, 4, 0, 2>, kFastGelu>(args...);
+    case 32: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 1, 4, 0, 2>, kFastGelu>(args...);
+    case 33: return launch_sdd_dma<DmaCfg<128, 512, 32, 3, 1, 4, 0, 2>, kFastGelu>(args...);
+    case 34: return launch_sdd_dma<DmaCfg<128, 256, 32, 3, 2, 4, 0, 2>, kFastGelu>(args...);
+    case 35: return launch_sdd_dma<DmaCfg<128, 256, 32, 3, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 36: return launch_sdd_dma<DmaCfg<128, 256, 64, 2, 2, 4, 0, 2>, kFastGelu>(args...);
     default: return fail(SB_ERR_INVALID, "sdd: unknown tile variant %d", variant);
   }
 }
@@ -302,9 +318,12 @@ extern "C" int sb_sdd(const void* x, const void* w1, const int32_t* row_token, c
   const hipStream_t s = as_stream(stream);
   const int forced = tuning_override("SPARSEBENCH_SDD_VARIANT");
   const int gelu_mode = tuning_override("SPARSEBENCH_GELU_LIBM");
-  // Default: 128 x 128 tiles on the LDS-DMA loop, two stages (64 KB LDS, two
-  // workgroups per CU): the fastest measured on every benchmark shape.
-  const int variant = forced > 0 ? forced : 11;
+  // Default, from timing every variant on the benchmark shapes (MI355X):
+  // 128 x 256 tiles, 8 waves, 3-stage LDS-DMA ring with non-temporal weight
+  // loads; with a deep reduction (D >= 4096) 128 x 512 tiles, 4 waves,
+  // BK 32 x 4 stages, which halve the x re-reads per FLOP.
+  int variant = forced > 0 ? forced : (d_model >= 4096 ? 32 : 25);
+  if (ffn_dim % 512 != 0 && variant >= 31 && variant <= 33) variant = 25;
   if (gelu_mode > 0)
     return dispatch_sdd<false>(variant, x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model,
                                ffn_dim, num_experts, num_row_blocks, apply_gelu, s);

@@ -17,7 +17,7 @@ from sparsebench_amd.workloads import routing_case
 pytestmark = pytest.mark.gpu
 
 TOL = {"rtol": 1.6e-2, "atol": 1.6e-2}
-VARIANTS = [1, 2, 3, 4, 5, 6, 7, 8, 11, 12, 13, 14, 15, 16, 17, 18, 19]
+VARIANTS = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 21, 22, 23, 24, 25, 26, 27, 31, 32, 33, 34, 35, 36]
 
 
 @pytest.mark.parametrize("variant", VARIANTS)

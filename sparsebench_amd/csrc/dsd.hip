@@ -125,8 +125,10 @@ struct DsdDmaSrc {
   const int32_t* col_indices;
   int64_t w_rows;
   int32_t d_model, begin;
-  uint32_t a_voff[Cfg::kAInstr];
-  uint32_t b_voff[Cfg::kBInstr];
+  uint32_t a_off[Cfg::kAInstr];
+  uint32_t b_off[Cfg::kBInstr];
+  __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
+  __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
   __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
     const int32_t p = begin + t / kStepsPerBlock;
     *r = make_rsrc(blocks + static_cast<int64_t>(p) * Cfg::BM * Cfg::BM, Cfg::BM * Cfg::BM * 2);
@@ -180,11 +182,11 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   src.begin = begin;
   const ADmaPos<Cfg> ap;
 #pragma unroll
-  for (int q = 0; q < Cfg::kAInstr; ++q) src.a_voff[q] = (ap.row[q] * BM + ap.chunk[q] * 8) * 2u;
+  for (int q = 0; q < Cfg::kAInstr; ++q) src.a_off[q] = (ap.row[q] * BM + ap.chunk[q] * 8) * 2u;
   const BDmaPos<Cfg> bp;
 #pragma unroll
   for (int q = 0; q < Cfg::kBInstr; ++q)
-    src.b_voff[q] = (static_cast<uint32_t>(bp.row[q]) * d_model + bp.col[q]) * 2u;
+    src.b_off[q] = (static_cast<uint32_t>(bp.row[q]) * d_model + bp.col[q]) * 2u;
 
   typename ML::Acc acc;
   ML::run(lds, src, (end - begin) * DsdDmaSrc<Cfg>::kStepsPerBlock, acc);
@@ -201,6 +203,164 @@ __global__ void __launch_bounds__(Cfg::kThreads)
             u32x2_t{pack_bf16x2(a[4 * g], a[4 * g + 1]), pack_bf16x2(a[4 * g + 2], a[4 * g + 3])};
       }
     }
+}
+
+// Persistent form (DmaMainloop::run_tiles): about one workgroup per CU slot,
+// each walking the tile list with stride gridDim.x through the same XCD
+// remap and grouped order as the one-tile kernel. A dead tile with
+// zero_dead_rows set is a tile of zero K steps: its epilogue writes zeros.
+template <class Cfg>
+struct DsdTiles {
+  using ML = DmaMainloop<Cfg>;
+  static constexpr int BM = Cfg::BM, BN = Cfg::BN;
+  static constexpr int kStepsPerBlock = BM / Cfg::BK;
+  struct Tile {
+    int steps;
+    int32_t begin;
+    int32_t rb;
+    int n0;
+  };
+  struct Src {
+    const uint16_t* blocks;
+    const uint16_t* w;
+    const int32_t* col_indices;
+    int64_t w_rows;
+    int32_t d_model, begin;
+    uint32_t n0_bytes;
+    uint32_t a_off[Cfg::kAInstr];
+    uint32_t b_off[Cfg::kBInstr];
+    __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+      const int32_t p = begin + t / kStepsPerBlock;
+      *r = make_rsrc(blocks + static_cast<int64_t>(p) * BM * BM, BM * BM * 2);
+      *s = static_cast<uint32_t>(t % kStepsPerBlock) * (Cfg::BK * 2);
+    }
+    __device__ __forceinline__ void b_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+      const int32_t p = begin + t / kStepsPerBlock;
+      const int64_t row0 = static_cast<int64_t>(col_indices[p]) * BM;
+      const bool ok = row0 >= 0 && row0 + BM <= w_rows;
+      *r = make_rsrc(w + (ok ? row0 : 0) * d_model, ok ? static_cast<uint32_t>(BM) * d_model * 2u : 0u);
+      *s = static_cast<uint32_t>(t % kStepsPerBlock) * (Cfg::BK * 2u) * static_cast<uint32_t>(d_model) + n0_bytes;
+    }
+    __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
+    __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
+  };
+
+  const uint16_t* blocks;
+  const uint16_t* w;
+  const int32_t* row_offsets;
+  const int32_t* col_indices;
+  uint16_t* out;
+  int64_t nnz, w_rows;
+  int32_t num_row_blocks, d_model, num_slices, zero_dead_rows, group;
+  int live_rb, live_tiles, vtile;
+  uint32_t a_off[Cfg::kAInstr];
+  uint32_t b_off[Cfg::kBInstr];
+
+  __device__ __forceinline__ void init() {
+    const ADmaPos<Cfg> ap;
+#pragma unroll
+    for (int q = 0; q < Cfg::kAInstr; ++q) a_off[q] = (ap.row[q] * BM + ap.chunk[q] * 8) * 2u;
+    const BDmaPos<Cfg> bp;
+#pragma unroll
+    for (int q = 0; q < Cfg::kBInstr; ++q) b_off[q] = (static_cast<uint32_t>(bp.row[q]) * d_model + bp.col[q]) * 2u;
+  }
+
+  __device__ __forceinline__ Src source(const Tile& t) const {
+    Src src;
+    src.blocks = blocks;
+    src.w = w;
+    src.col_indices = col_indices;
+    src.w_rows = w_rows;
+    src.d_model = d_model;
+    src.begin = t.begin;
+    src.n0_bytes = static_cast<uint32_t>(t.n0) * 2u;
+#pragma unroll
+    for (int q = 0; q < Cfg::kAInstr; ++q) src.a_off[q] = a_off[q];
+#pragma unroll
+    for (int q = 0; q < Cfg::kBInstr; ++q) src.b_off[q] = b_off[q];
+    return src;
+  }
+
+  __device__ __forceinline__ bool next(Tile& t) {
+    while (vtile < live_tiles) {
+      const int tile = xcd_remap(vtile, live_tiles);
+      vtile += gridDim.x;
+      int rb, slice;
+      tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
+      int32_t begin = row_offsets[rb];
+      int32_t end = row_offsets[rb + 1];
+      if (begin < 0 || end > nnz || end < begin) begin = end = 0;  // not a BSR row: treat as empty
+      if (begin == end && !zero_dead_rows) continue;
+      t.rb = __builtin_amdgcn_readfirstlane(rb);
+      t.n0 = __builtin_amdgcn_readfirstlane(slice * BN);
+      t.begin = __builtin_amdgcn_readfirstlane(begin);
+      t.steps = __builtin_amdgcn_readfirstlane((end - begin) * kStepsPerBlock);
+      return true;
+    }
+    return false;
+  }
+
+  __device__ __forceinline__ void epilogue(const Tile& t, typename ML::Acc& acc) const {
+    uint16_t* out_tile = out + static_cast<int64_t>(t.rb) * BM * d_model + t.n0;
+#pragma unroll
+    for (int jn = 0; jn < Cfg::TN; ++jn)
+#pragma unroll
+      for (int i = 0; i < Cfg::TM; ++i) {
+        uint16_t* row = out_tile + static_cast<int64_t>(ML::out_row(i)) * d_model;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x16_t& a = acc[jn][i];
+          *reinterpret_cast<u32x2_t*>(row + ML::out_col(jn, g)) =
+              u32x2_t{pack_bf16x2(a[4 * g], a[4 * g + 1]), pack_bf16x2(a[4 * g + 2], a[4 * g + 3])};
+        }
+      }
+  }
+};
+
+template <class Cfg>
+__global__ void __launch_bounds__(Cfg::kThreads)
+    dsd_persistent_kernel(const uint16_t* __restrict__ blocks, const uint16_t* __restrict__ w,
+                          const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ col_indices,
+                          uint16_t* __restrict__ out, int64_t nnz, int64_t w_rows, int32_t num_row_blocks,
+                          int32_t d_model, int32_t num_slices, int32_t zero_dead_rows, int32_t group) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+  DsdTiles<Cfg> sched;
+  sched.blocks = blocks;
+  sched.w = w;
+  sched.row_offsets = row_offsets;
+  sched.col_indices = col_indices;
+  sched.out = out;
+  sched.nnz = nnz;
+  sched.w_rows = w_rows;
+  sched.num_row_blocks = num_row_blocks;
+  sched.d_model = d_model;
+  sched.num_slices = num_slices;
+  sched.zero_dead_rows = zero_dead_rows;
+  sched.group = group;
+  sched.live_rb = zero_dead_rows ? num_row_blocks : live_row_blocks(row_offsets, num_row_blocks);
+  sched.live_tiles = sched.live_rb * num_slices;
+  sched.vtile = blockIdx.x;
+  sched.init();
+  DmaMainloop<Cfg>::run_tiles(lds, sched);
+}
+
+template <class Cfg>
+int launch_dsd_persistent(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices,
+                          void* out, int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t d_model,
+                          int32_t zero_dead_rows, hipStream_t stream) {
+  if (d_model % Cfg::BN != 0) return fail(SB_ERR_INVALID, "dsd: D %% tile width != 0");
+  const int32_t num_slices = static_cast<int32_t>(d_model / Cfg::BN);
+  const int64_t tiles = num_row_blocks * num_slices;
+  static int occupancy = 0;
+  int grid = 0;
+  if (const int rc = persistent_grid(reinterpret_cast<const void*>(dsd_persistent_kernel<Cfg>), Cfg::kThreads, tiles,
+                                     &occupancy, &grid))
+    return rc;
+  dsd_persistent_kernel<Cfg><<<static_cast<uint32_t>(grid), Cfg::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(blocks), static_cast<const uint16_t*>(w), row_offsets, col_indices,
+      static_cast<uint16_t*>(out), nnz, w_rows, static_cast<int32_t>(num_row_blocks), static_cast<int32_t>(d_model),
+      num_slices, zero_dead_rows, tile_group());
+  return check_launch("dsd");
 }
 
 template <class Cfg>
@@ -279,6 +439,15 @@ int dispatch_dsd(int variant, Args... args) {
     case 36:
       if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 4, 0, 2>>(args...);
       else return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 2, 0, 2>>(args...);
+    case 41:
+      if constexpr (BM == 128) return launch_dsd_persistent<DmaCfg<BM, 256, 64, 3, 2, 4, 0, 2>>(args...);
+      else return launch_dsd_persistent<DmaCfg<BM, 256, 64, 3, 2, 2, 0, 2>>(args...);
+    case 42: return launch_dsd_persistent<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2>>(args...);
+    case 43: return launch_dsd_persistent<DmaCfg<BM, 128, 64, 2, 2, 2, 0, 2>>(args...);
+    case 44:
+      if constexpr (BM == 128) return launch_dsd_persistent<DmaCfg<BM, 256, 32, 3, 2, 4, 0, 2>>(args...);
+      else return launch_dsd_persistent<DmaCfg<BM, 256, 32, 3, 2, 2, 0, 2>>(args...);
+    case 45: return launch_dsd_persistent<DmaCfg<BM, 128, 64, 2>>(args...);
     default: return fail(SB_ERR_INVALID, "dsd: unknown tile variant %d", variant);
   }
 }
@@ -311,16 +480,20 @@ extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offs
   const int forced = tuning_override("SPARSEBENCH_DSD_VARIANT");
   // Default, from timing every variant on the benchmark shapes (MI355X):
   // 128 x 512 tiles, 4 waves, BK 32 x 4-stage LDS-DMA ring with non-temporal
-  // W loads. With a deep reduction (row K = F per expert >= 8192, read from
-  // the buffer shape: nnz / num_row_blocks blocks per row) there are enough
-  // K steps per tile that 128 x 128 tiles balance the CUs better.
+  // W loads. The row's reduction depth (K = F per expert, read from the
+  // buffer shape: nnz / num_row_blocks blocks per row) moves the choice:
+  // with K >= 8192 there are enough K steps per tile that 128 x 128 tiles
+  // balance the CUs better; with K < 2048 a tile is so short that its
+  // prologue and epilogue matter, and the persistent 128 x 256 form, which
+  // overlaps them with the next tile's loads, wins.
   const int64_t row_k = num_row_blocks > 0 ? nnz / num_row_blocks * block_size : 0;
-  int variant = forced > 0 ? forced : (row_k >= 8192 ? 11 : 32);
+  int variant = forced > 0 ? forced : (row_k >= 8192 ? 11 : row_k < 2048 ? 41 : 32);
   if (d_model % 256 != 0 && (variant == 2 || variant == 4 || variant == 5 || variant == 6 || variant == 14 ||
                              variant == 15 || variant == 16 || variant == 17 || variant == 24 || variant == 25 ||
-                             variant == 26 || variant == 34 || variant == 35 || variant == 36))
+                             variant == 26 || variant == 34 || variant == 35 || variant == 36 || variant == 41 ||
+                             variant == 44))
     variant = 1;
-  if (d_model % 512 != 0 && variant >= 31 && variant <= 33) variant = d_model % 256 == 0 ? 25 : 21;
+  if (d_model % 512 != 0 && ((variant >= 31 && variant <= 33) || variant == 42)) variant = d_model % 256 == 0 ? 25 : 21;
   if (block_size == 128)
     return dispatch_dsd<128>(variant, blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
                              zero_dead_rows, s);

@@ -147,7 +147,8 @@ __device__ __forceinline__ void wait_steps(int later) {
 
 // Per-step sources, supplied by the kernel:
 //   a_src(t, &rsrc, &soffset), b_src(t, &rsrc, &soffset)
-// and fixed per-lane offsets a_voff[kAInstr], b_voff[kBInstr] (bytes).
+// and fixed per-lane offsets a_voff(q), q < kAInstr, b_voff(q), q < kBInstr
+// (bytes).
 template <class Cfg>
 struct DmaMainloop {
   using Acc = f32x16_t[Cfg::TN][Cfg::TM];  // acc[j][i]: C^T block (n block j, m block i)
@@ -156,22 +157,28 @@ struct DmaMainloop {
   // the DMA of step t+STAGES-1 writes a different stage than the one step t
   // reads, and saying so lets the compiler drop the vmcnt(0) it would
   // otherwise put before every LDS read (which serializes loads and MFMAs).
+  // The DMA of K step `t` of `src` into ring slot `ring % STAGES`.
   template <class Src>
-  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int t, const Src& src) {
+  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int ring, int t, const Src& src) {
     const int wave = threadIdx.x >> 6;
-    uint8_t* stage = lds + (t % Cfg::STAGES) * Cfg::kStageBytes;
+    uint8_t* stage = lds + (ring % Cfg::STAGES) * Cfg::kStageBytes;
     __amdgpu_buffer_rsrc_t ra, rb;
     uint32_t sa, sb;
     src.a_src(t, &ra, &sa);
     src.b_src(t, &rb, &sb);
+    // The scalar offsets are uniform by contract; saying so keeps the
+    // compiler from wrapping each load in a per-lane waterfall loop when it
+    // cannot prove it.
+    sa = __builtin_amdgcn_readfirstlane(sa);
+    sb = __builtin_amdgcn_readfirstlane(sb);
 #pragma unroll
     for (int q = 0; q < Cfg::kAInstr; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024), 16,
-                                               src.a_voff[q], sa, 0, Cfg::CPA);
+                                               src.a_voff(q), sa, 0, Cfg::CPA);
 #pragma unroll
     for (int q = 0; q < Cfg::kBInstr; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q) * 1024), 16, src.b_voff[q], sb, 0, Cfg::CPB);
+          rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q) * 1024), 16, src.b_voff(q), sb, 0, Cfg::CPB);
   }
 
   __device__ __forceinline__ static void compute(const uint8_t* __restrict__ stage, Acc& acc) {
@@ -233,7 +240,7 @@ struct DmaMainloop {
     if (num_steps <= 0) return;
 #pragma unroll
     for (int s = 0; s < Cfg::STAGES - 1; ++s)
-      if (s < num_steps) issue(lds, s, src);
+      if (s < num_steps) issue(lds, s, s, src);
     for (int t = 0; t < num_steps; ++t) {
       // Step t's loads are complete once at most the later issued steps
       // (t+1 .. t+STAGES-2, if they exist) are outstanding.
@@ -241,8 +248,76 @@ struct DmaMainloop {
       // Every wave's step-t data is in LDS, and every wave is done with
       // step t-1's stage, which the next issue overwrites.
       __builtin_amdgcn_s_barrier();
-      if (t + Cfg::STAGES - 1 < num_steps) issue(lds, t + Cfg::STAGES - 1, src);
+      if (t + Cfg::STAGES - 1 < num_steps) issue(lds, t + Cfg::STAGES - 1, t + Cfg::STAGES - 1, src);
       compute(lds + (t % Cfg::STAGES) * Cfg::kStageBytes, acc);
+    }
+  }
+
+  // Persistent form: one workgroup runs a sequence of tiles, and the ring
+  // runs straight across tile boundaries. The last STAGES-1 steps of a tile
+  // issue the first steps of the next one, so its loads are in flight while
+  // this tile's epilogue runs, and no tile starts with an empty pipeline.
+  //
+  // Sched supplies
+  //   Tile                       a tile: `steps`, its number of K steps
+  //                              (may be 0), plus what its sources need
+  //   bool next(Tile&)           this workgroup's next tile; false when none
+  //   Src source(const Tile&)    the tile's step sources, as for run(), by value
+  //   void epilogue(const Tile&, Acc&)
+  // Tile metadata should be read with wave-uniform (scalar) loads: a vector
+  // load would make the compiler wait on the whole DMA queue at its use.
+  //
+  // Waits: step g's loads are done once at most the loads of the steps
+  // issued after it are outstanding. Buffer loads complete in issue order,
+  // so epilogue stores issued between them only make the wait stricter.
+  template <class Sched>
+  __device__ __forceinline__ static void run_tiles(uint8_t* lds, Sched& sched) {
+    using Tile = typename Sched::Tile;
+    Tile cur, nxt;
+    if (!sched.next(cur)) return;
+    bool has_nxt = sched.next(nxt);
+    // Issue cursor: tile slot (0 = cur, 1 = nxt) and that tile's next step.
+    int slot = 0, ik = 0;
+    int issued = 0, done = 0;  // steps issued / computed by this workgroup
+    auto issue_next = [&]() {
+      if (slot == 0 && ik >= cur.steps) {
+        if (!has_nxt) return;
+        slot = 1;
+        ik = 0;
+      }
+      if (slot == 1 && ik >= nxt.steps) return;
+      // By value: the choice is a uniform select, not a pointer into the
+      // two tiles (which would move them to scratch).
+      const auto src = slot == 0 ? sched.source(cur) : sched.source(nxt);
+      issue(lds, issued, ik, src);
+      ++ik;
+      ++issued;
+    };
+#pragma unroll
+    for (int s = 0; s < Cfg::STAGES - 1; ++s) issue_next();
+    while (true) {
+      Acc acc;
+#pragma unroll
+      for (int jn = 0; jn < Cfg::TN; ++jn)
+#pragma unroll
+        for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[jn][i][v] = 0.0f;
+      for (int k = 0; k < cur.steps; ++k, ++done) {
+        wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(issued - done - 1);
+        __builtin_amdgcn_s_barrier();
+        issue_next();
+        compute(lds + (done % Cfg::STAGES) * Cfg::kStageBytes, acc);
+      }
+      sched.epilogue(cur, acc);
+      if (!has_nxt) break;
+      cur = nxt;
+      if (slot == 1) {
+        slot = 0;  // ik already counts the new cur's issued steps
+      } else {
+        ik = 0;  // nothing of it issued yet
+      }
+      has_nxt = sched.next(nxt);
     }
   }
 

@@ -137,9 +137,11 @@ __global__ void __launch_bounds__(Cfg::kThreads)
 template <class Cfg>
 struct SddDmaSrc {
   __amdgpu_buffer_rsrc_t x_rsrc, w_rsrc;
-  uint32_t a_voff[Cfg::kAInstr];
-  uint32_t b_voff[Cfg::kBInstr];
+  uint32_t a_off[Cfg::kAInstr];
+  uint32_t b_off[Cfg::kBInstr];
   uint32_t b_step_bytes;
+  __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
+  __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
   __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
     *r = x_rsrc;
     *s = static_cast<uint32_t>(t) * (Cfg::BK * 2);
@@ -185,14 +187,14 @@ __global__ void __launch_bounds__(Cfg::kThreads)
 #pragma unroll
   for (int q = 0; q < Cfg::kAInstr; ++q) {
     const int32_t tok = row_token[static_cast<int64_t>(rb) * kBS + ap.row[q]];
-    src.a_voff[q] = (tok >= 0 && tok < num_tokens)
+    src.a_off[q] = (tok >= 0 && tok < num_tokens)
                         ? static_cast<uint32_t>(tok) * static_cast<uint32_t>(d_model) * 2u + ap.chunk[q] * 16u
                         : kOutOfRange;
   }
   const BDmaPos<Cfg> bp;
 #pragma unroll
   for (int q = 0; q < Cfg::kBInstr; ++q)
-    src.b_voff[q] = (static_cast<uint32_t>(bp.row[q]) * ffn_dim + n0 + bp.col[q]) * 2u;
+    src.b_off[q] = (static_cast<uint32_t>(bp.row[q]) * ffn_dim + n0 + bp.col[q]) * 2u;
 
   typename ML::Acc acc;
   ML::run(lds, src, d_model / Cfg::BK, acc);
@@ -217,6 +219,203 @@ __global__ void __launch_bounds__(Cfg::kThreads)
             u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       }
     }
+}
+
+// Persistent form (DmaMainloop::run_tiles): gridDim.x workgroups, about one
+// per CU slot, each walking the tile list with stride gridDim.x through the
+// same XCD remap and grouped order as the one-tile-per-workgroup kernel.
+template <class Cfg, bool kFastGelu>
+struct SddTiles {
+  using ML = DmaMainloop<Cfg>;
+  static constexpr int BN = Cfg::BN;
+  // Per tile: the expert's W1 buffer, the column origin and this lane's
+  // gathered x rows. Everything else is shared by all tiles.
+  struct Tile {
+    __amdgpu_buffer_rsrc_t w_rsrc;
+    uint32_t a_off[Cfg::kAInstr];
+    int steps;
+    int32_t begin;
+    int n0;
+  };
+  struct Src {
+    __amdgpu_buffer_rsrc_t x_rsrc, w_rsrc;
+    uint32_t b_step_bytes, n0_bytes;
+    uint32_t a_off[Cfg::kAInstr];
+    uint32_t b_off[Cfg::kBInstr];
+    __device__ __forceinline__ void a_src(int k, __amdgpu_buffer_rsrc_t* r, uint32_t* off) const {
+      *r = x_rsrc;
+      *off = static_cast<uint32_t>(k) * (Cfg::BK * 2);
+    }
+    __device__ __forceinline__ void b_src(int k, __amdgpu_buffer_rsrc_t* r, uint32_t* off) const {
+      *r = w_rsrc;
+      *off = static_cast<uint32_t>(k) * b_step_bytes + n0_bytes;
+    }
+    __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
+    __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
+  };
+
+  const uint16_t* x;
+  const uint16_t* w1;
+  const int32_t* row_token;
+  const int32_t* row_block_expert;
+  const int32_t* row_offsets;
+  uint16_t* out;
+  int32_t num_tokens, d_model, ffn_dim, num_experts, num_row_blocks, num_slices, apply_gelu, group;
+  int live_rb, live_tiles, vtile;
+  __amdgpu_buffer_rsrc_t x_rsrc;
+  uint32_t b_step_bytes;
+  uint32_t b_off[Cfg::kBInstr];  // this lane's W1 chunk at column origin 0
+
+  __device__ __forceinline__ void init() {
+    x_rsrc = make_rsrc(x, static_cast<uint32_t>(num_tokens) * static_cast<uint32_t>(d_model) * 2u);
+    b_step_bytes = static_cast<uint32_t>(Cfg::BK) * static_cast<uint32_t>(ffn_dim) * 2u;
+    const BDmaPos<Cfg> bp;
+#pragma unroll
+    for (int q = 0; q < Cfg::kBInstr; ++q) b_off[q] = (static_cast<uint32_t>(bp.row[q]) * ffn_dim + bp.col[q]) * 2u;
+  }
+
+  __device__ __forceinline__ Src source(const Tile& t) const {
+    Src src;
+    src.x_rsrc = x_rsrc;
+    src.w_rsrc = t.w_rsrc;
+    src.b_step_bytes = b_step_bytes;
+    src.n0_bytes = static_cast<uint32_t>(t.n0) * 2u;
+#pragma unroll
+    for (int q = 0; q < Cfg::kAInstr; ++q) src.a_off[q] = t.a_off[q];
+#pragma unroll
+    for (int q = 0; q < Cfg::kBInstr; ++q) src.b_off[q] = b_off[q];
+    return src;
+  }
+
+  // This lane's token for A DMA instruction q. The wave's rows are
+  // consecutive: kAInstr * kARowsPerInstr of them, read with uniform
+  // (scalar) loads and picked per lane with selects.
+  __device__ __forceinline__ void lane_tokens(int rb, int32_t (&tok)[Cfg::kAInstr]) const {
+    constexpr int kRows = Cfg::kAInstr * Cfg::kARowsPerInstr;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int32_t* rows = row_token + static_cast<int64_t>(rb) * kBS + wave * kRows;
+    // readfirstlane pins each value to an SGPR: without it the compiler folds
+    // the selects into one per-lane vector load, whose wait (vmcnt) would
+    // also wait for the whole DMA queue.
+    int32_t wt[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) wt[r] = __builtin_amdgcn_readfirstlane(rows[r]);
+    const int lr = (threadIdx.x & 63) / Cfg::kAChunksPerRow;
+#pragma unroll
+    for (int q = 0; q < Cfg::kAInstr; ++q) {
+      int32_t v = wt[q * Cfg::kARowsPerInstr];
+#pragma unroll
+      for (int r = 1; r < Cfg::kARowsPerInstr; ++r) v = lr == r ? wt[q * Cfg::kARowsPerInstr + r] : v;
+      tok[q] = v;
+    }
+  }
+
+  __device__ __forceinline__ bool next(Tile& t) {
+    const int32_t ffn_blocks = ffn_dim / kBS;
+    while (vtile < live_tiles) {
+      const int tile = xcd_remap(vtile, live_tiles);
+      vtile += gridDim.x;
+      int rb, slice;
+      tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
+      const int32_t begin = row_offsets[rb];
+      const int32_t end = row_offsets[rb + 1];
+      const int32_t expert = row_block_expert[rb];
+      // Same skips as the one-tile kernel: dead, or not a routing layout.
+      if (begin == end || end - begin != ffn_blocks || begin < 0 || end > num_row_blocks * ffn_blocks ||
+          expert < 0 || expert >= num_experts)
+        continue;
+      // Uniform by construction; readfirstlane keeps them in SGPRs (a VGPR
+      // n0 would make the buffer offset of every W load lane-divergent).
+      t.n0 = __builtin_amdgcn_readfirstlane(slice * BN);
+      t.begin = __builtin_amdgcn_readfirstlane(begin);
+      t.steps = d_model / Cfg::BK;
+      t.w_rsrc = make_rsrc(w1 + static_cast<int64_t>(expert) * d_model * ffn_dim,
+                           static_cast<uint32_t>(d_model) * static_cast<uint32_t>(ffn_dim) * 2u);
+      int32_t tok[Cfg::kAInstr];
+      lane_tokens(rb, tok);
+      const ADmaPos<Cfg> ap;
+#pragma unroll
+      for (int q = 0; q < Cfg::kAInstr; ++q)
+        t.a_off[q] = (tok[q] >= 0 && tok[q] < num_tokens)
+                         ? static_cast<uint32_t>(tok[q]) * static_cast<uint32_t>(d_model) * 2u + ap.chunk[q] * 16u
+                         : kOutOfRange;
+      return true;
+    }
+    return false;
+  }
+
+  __device__ __forceinline__ void epilogue(const Tile& t, typename ML::Acc& acc) const {
+    uint16_t* blocks = out + static_cast<int64_t>(t.begin) * kBS * kBS;
+#pragma unroll
+    for (int jn = 0; jn < Cfg::TN; ++jn)
+#pragma unroll
+      for (int i = 0; i < Cfg::TM; ++i) {
+        const int m = ML::out_row(i);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int f = t.n0 + ML::out_col(jn, g);
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = acc[jn][i][4 * g + e];
+            if (apply_gelu) v[e] = kFastGelu ? gelu_erf_fast(v[e]) : gelu_erf_libm(v[e]);
+          }
+          *reinterpret_cast<u32x2_t*>(blocks + static_cast<int64_t>(f / kBS) * kBS * kBS + m * kBS + (f % kBS)) =
+              u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        }
+      }
+  }
+};
+
+template <class Cfg, bool kFastGelu>
+__global__ void __launch_bounds__(Cfg::kThreads)
+    sdd_persistent_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
+                          const int32_t* __restrict__ row_token, const int32_t* __restrict__ row_block_expert,
+                          const int32_t* __restrict__ row_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
+                          int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t num_row_blocks,
+                          int32_t num_slices, int32_t apply_gelu, int32_t group) {
+  static_assert(Cfg::BM == kBS, "one row block per tile");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+  SddTiles<Cfg, kFastGelu> sched;
+  sched.x = x;
+  sched.w1 = w1;
+  sched.row_token = row_token;
+  sched.row_block_expert = row_block_expert;
+  sched.row_offsets = row_offsets;
+  sched.out = out;
+  sched.num_tokens = num_tokens;
+  sched.d_model = d_model;
+  sched.ffn_dim = ffn_dim;
+  sched.num_experts = num_experts;
+  sched.num_row_blocks = num_row_blocks;
+  sched.num_slices = num_slices;
+  sched.apply_gelu = apply_gelu;
+  sched.group = group;
+  sched.live_rb = live_row_blocks(row_offsets, num_row_blocks);
+  sched.live_tiles = sched.live_rb * num_slices;
+  sched.vtile = blockIdx.x;
+  sched.init();
+  DmaMainloop<Cfg>::run_tiles(lds, sched);
+}
+
+template <class Cfg, bool kFastGelu>
+int launch_sdd_persistent(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+                          const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
+                          int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, hipStream_t stream) {
+  if (ffn_dim % Cfg::BN != 0) return fail(SB_ERR_INVALID, "sdd: F %% tile width != 0");
+  const int32_t num_slices = static_cast<int32_t>(ffn_dim / Cfg::BN);
+  const int64_t tiles = num_row_blocks * num_slices;
+  static int occupancy = 0;
+  int grid = 0;
+  if (const int rc = persistent_grid(reinterpret_cast<const void*>(sdd_persistent_kernel<Cfg, kFastGelu>),
+                                     Cfg::kThreads, tiles, &occupancy, &grid))
+    return rc;
+  sdd_persistent_kernel<Cfg, kFastGelu><<<static_cast<uint32_t>(grid), Cfg::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
+      static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens), static_cast<int32_t>(d_model),
+      static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts), static_cast<int32_t>(num_row_blocks),
+      num_slices, apply_gelu, tile_group());
+  return check_launch("sdd");
 }
 
 template <class Cfg, bool kFastGelu>
@@ -284,6 +483,9 @@ int dispatch_sdd(int variant, Args... args) {
     case 34: return launch_sdd_dma<DmaCfg<128, 256, 32, 3, 2, 4, 0, 2>, kFastGelu>(args...);
     case 35: return launch_sdd_dma<DmaCfg<128, 256, 32, 3, 2, 2, 0, 2>, kFastGelu>(args...);
     case 36: return launch_sdd_dma<DmaCfg<128, 256, 64, 2, 2, 4, 0, 2>, kFastGelu>(args...);
+    case 41: return launch_sdd_persistent<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2>, kFastGelu>(args...);
+    case 43: return launch_sdd_persistent<DmaCfg<128, 128, 64, 2, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 44: return launch_sdd_persistent<DmaCfg<128, 256, 32, 3, 2, 4, 0, 2>, kFastGelu>(args...);
     default: return fail(SB_ERR_INVALID, "sdd: unknown tile variant %d", variant);
   }
 }

@@ -94,6 +94,79 @@ int sb_combine(const void* y, const int32_t* copy_row, const void* gates, int32_
                int64_t num_tokens, int32_t k, int64_t d_model, int64_t y_rows, const int32_t* valid_tokens,
                void* stream);
 
+/* ---- Routing given as assignments (sparsebench/moe.py:59-91) ---------- */
+
+/* Replaces the routing of moe_forward_assigned (sparsebench/moe.py:77-82:
+ * route_device on expert_of_copy as [N, 1], then row_token remapped from
+ * copy index to token). Copy c sends token_of_copy[c] (int32/int64) to
+ * expert_of_copy[c] (int32/int64). The outputs are those of sb_routing with
+ * T*k replaced by N = num_copies and row_token holding token ids; size them
+ * with sb_routing_sizes(N, ...). A token id outside [0, num_tokens) is
+ * treated like a bad expert id (copy skipped, error = 1); the reference
+ * would index out of range there. valid_tokens: as for sb_routing, with the
+ * copy's token id compared to T'. */
+int sb_routing_assigned(const void* expert_of_copy, int32_t expert_is_i64, const void* token_of_copy,
+                        int32_t token_is_i64, int64_t num_copies, int64_t num_tokens, int32_t num_experts,
+                        int32_t ffn_dim, int32_t block_size, const int32_t* valid_tokens, int32_t* workspace,
+                        int32_t* tokens_per_expert, int32_t* padded_offsets, int32_t* row_token, int32_t* copy_row,
+                        int32_t* row_block_expert, int32_t* row_offsets, int32_t* col_indices, int32_t* error,
+                        void* stream);
+
+/* Each token's copies, for the assigned combine (the grouping that the
+ * reference leaves to index_add_ at sparsebench/moe.py:89-91). Writes
+ * token_offsets[T+1] and token_copies[N]: the copies of token t are
+ * token_copies[token_offsets[t] .. token_offsets[t+1]), in ascending copy
+ * order; copies with copy_row < 0 are left out and the unused tail of
+ * token_copies is -1. One workgroup; deterministic. */
+int sb_token_csr(const void* token_of_copy, int32_t token_is_i64, const int32_t* copy_row, int64_t num_copies,
+                 int64_t num_tokens, int32_t* token_offsets, int32_t* token_copies, void* stream);
+
+/* Replaces the combine of moe_forward_assigned (sparsebench/moe.py:89-91).
+ * out[t, :] = bf16( sum over t's copies c, in token_copies order, of
+ * fp32(y[copy_row[c], :]) * fp32(weights[c]) ); zeros for a token with no
+ * copy. token_copies may be NULL when the copies are already in token order
+ * (then copy i of the range is c = i). weights [N] of weight_dtype.
+ * valid_tokens: NULL, or a device int32 T' <= T: rows t >= T' not written. */
+int sb_combine_assigned(const void* y, const int32_t* copy_row, const void* weights, int32_t weight_dtype,
+                        const int32_t* token_offsets, const int32_t* token_copies, void* out, int64_t num_tokens,
+                        int64_t d_model, int64_t y_rows, const int32_t* valid_tokens, void* stream);
+
+/* ---- Router: top-k and token rounding (sparsebench/token_rounding.py) -- */
+
+/* Sizes for token rounding of scores [T, E] at top-k with the given tile,
+ * and the layout (block_size, ffn_dim) built from it: the list capacity
+ * (N <= min(T*E, T*k + E*(tile/2)): an expert moves up by less than half a
+ * tile), the layout's worst-case row blocks / rows (sb_routing_sizes of the
+ * capacity) and the int32 workspace of sb_token_rounding. Host-only. */
+int sb_router_sizes(int64_t num_tokens, int32_t num_experts, int32_t k, int32_t tile, int32_t block_size,
+                    int32_t ffn_dim, int64_t* max_assignments, int64_t* max_row_blocks, int64_t* max_rows,
+                    int64_t* workspace_elems);
+
+/* Replaces top_k_assignments (sparsebench/token_rounding.py:42-49):
+ * scores [T, E] fp32 -> top_idx [T, k] int32, the k best experts of each
+ * token in descending score order (equal scores: lower expert first), and
+ * top_weight [T, k] fp32 = the picked scores over their sum. k <= 16. */
+int sb_router_topk(const float* scores, int64_t num_tokens, int32_t num_experts, int32_t k, int32_t* top_idx,
+                   float* top_weight, void* stream);
+
+/* Replaces token_rounding (sparsebench/token_rounding.py:61-85), fused with
+ * the routing of moe_forward_assigned, with no host sync.
+ * scores [T, E] fp32. Writes the rounded routing as a list in (token,
+ * expert) order, capacity max_assignments (sb_router_sizes):
+ *   token_of_copy, expert_of_copy (int32), weight_of_copy (fp32), entries
+ *   past the real length -1 / -1 / 0; num_assignments[1] = the length N;
+ *   token_offsets[T+1]: token t's copies are token_offsets[t] .. [t+1]
+ *   (pass NULL token_copies to sb_combine_assigned);
+ * and its block-sparse layout, as sb_routing_assigned would build it from
+ * that list (tokens_per_expert = the rounded counts; copy_row[capacity]).
+ * workspace: workspace_elems int32 (sb_router_sizes). E <= 1024, k <= 16. */
+int sb_token_rounding(const float* scores, int64_t num_tokens, int32_t num_experts, int32_t k, int32_t tile,
+                      int32_t block_size, int32_t ffn_dim, int32_t* workspace, int32_t* token_of_copy,
+                      int32_t* expert_of_copy, float* weight_of_copy, int32_t* num_assignments,
+                      int32_t* token_offsets, int32_t* tokens_per_expert, int32_t* padded_offsets,
+                      int32_t* row_token, int32_t* copy_row, int32_t* row_block_expert, int32_t* row_offsets,
+                      int32_t* col_indices, int32_t* error, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,6 +6,7 @@ Expert e computes y = gelu(x @ w1[e]) @ w2[e] with the exact erf GELU
 csrc/sdd.cu:41). Each token sums its k experts' outputs weighted by its gates.
 
     moe_reference            loop over experts (reference.py:49-61)
+    moe_assigned_reference   the same for a routing given as a list (moe.py:59-91)
     per_token_reference      one token at a time (tests/test_reference.py:18-27)
     moe_blocksparse_reference through the layout: group, SDD, GELU, DSD,
                              combine (reference.py:64-114)
@@ -64,6 +65,23 @@ def moe_reference(x, expert_idx, expert_weight, w1, w2) -> torch.Tensor:
         if token.numel():
             y = gelu_erf(x[token] @ w1[e]) @ w2[e]
             out.index_add_(0, token, y * expert_weight[token, slot, None])
+    return out
+
+
+def moe_assigned_reference(x, token, expert, weight, w1, w2) -> torch.Tensor:
+    """[T, D] fp32 for a routing given as a list: copy c sends token[c] to
+    expert[c] with weight[c]; tokens with no copy give 0 (the layer of
+    sparsebench/moe.py:59-91, as the reference's tests/test_token_rounding.py:
+    91-99 computes it). fp32 math on the given values, one expert at a time."""
+    x, w1, w2 = x.float().cpu(), w1.float().cpu(), w2.float().cpu()
+    token, expert = torch.as_tensor(token).long().cpu(), torch.as_tensor(expert).long().cpu()
+    weight = torch.as_tensor(weight).float().cpu()
+    out = torch.zeros(x.shape[0], x.shape[1])
+    for e in range(w1.shape[0]):
+        m = expert == e
+        if m.any():
+            y = gelu_erf(x[token[m]] @ w1[e]) @ w2[e]
+            out.index_add_(0, token[m], y * weight[m, None])
     return out
 
 

@@ -264,3 +264,171 @@ def combine_cuda(
         num_tokens, k, y.shape[1], y.shape[0], _ptr(valid_tokens), stream_of(y.device),
     ))
     return out
+
+
+# ---- routing given as assignments; router (this build's C ABI, no pybind11
+# counterpart in the reference: there these steps are torch code in
+# sparsebench/moe.py:59-91 and sparsebench/token_rounding.py) ----
+
+
+def _check_copy_list(t: torch.Tensor, name: str) -> None:
+    if not (t.is_cuda and t.dim() == 1 and t.dtype in (torch.int32, torch.int64) and t.is_contiguous()):
+        _fail(f"{name} must be a contiguous 1-D int32 or int64 CUDA tensor")
+
+
+def build_topology_assigned_cuda(
+    token_of_copy: torch.Tensor,
+    expert_of_copy: torch.Tensor,
+    num_tokens: int,
+    num_experts: int,
+    ffn_dim: int,
+    block_size: int,
+    valid_tokens: torch.Tensor | None = None,
+) -> list[torch.Tensor]:
+    """The routing of a flat list (copy c: token_of_copy[c] -> expert_of_copy[c]),
+    as build_topology_cuda with k = 1 and row_token holding token ids.
+    Same 8 outputs, sized for N = len(list). No host sync."""
+    _check_copy_list(token_of_copy, "token_of_copy")
+    _check_copy_list(expert_of_copy, "expert_of_copy")
+    n = expert_of_copy.numel()
+    if token_of_copy.numel() != n or n == 0:
+        _fail("token_of_copy and expert_of_copy must be non-empty and of the same length")
+    if token_of_copy.device != expert_of_copy.device:
+        _fail("token_of_copy and expert_of_copy must be on the same GPU")
+    if not 0 < num_tokens <= _I32_MAX:
+        _fail(f"num_tokens must be in [1, 2^31), got {num_tokens}")
+    if valid_tokens is not None:
+        if not (valid_tokens.is_cuda and valid_tokens.dtype == torch.int32 and valid_tokens.numel() == 1):
+            _fail("valid_tokens must be a one-element int32 CUDA tensor")
+    max_row_blocks, max_rows, ws = routing_sizes(n, num_experts, ffn_dim, block_size)
+    dev = expert_of_copy.device
+    opts = {"dtype": torch.int32, "device": dev}
+    workspace = torch.empty(ws, **opts)
+    outs = [torch.empty(num_experts, **opts), torch.empty(num_experts + 1, **opts), torch.empty(max_rows, **opts),
+            torch.empty(n, **opts), torch.empty(max_row_blocks, **opts), torch.empty(max_row_blocks + 1, **opts),
+            torch.empty(max_row_blocks * (ffn_dim // block_size), **opts), torch.empty(1, **opts)]
+    check(lib().sb_routing_assigned(
+        expert_of_copy.data_ptr(), 1 if expert_of_copy.dtype == torch.int64 else 0, token_of_copy.data_ptr(),
+        1 if token_of_copy.dtype == torch.int64 else 0, n, num_tokens, num_experts, ffn_dim, block_size,
+        _ptr(valid_tokens), workspace.data_ptr(), *(o.data_ptr() for o in outs), stream_of(dev),
+    ))
+    return outs
+
+
+def token_csr_cuda(token_of_copy: torch.Tensor, copy_row: torch.Tensor, num_tokens: int
+                   ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(token_offsets [T+1], token_copies [N]): each token's routed copies in
+    ascending copy order. Deterministic, no host sync."""
+    _check_copy_list(token_of_copy, "token_of_copy")
+    _check_index(copy_row, "copy_row")
+    n = token_of_copy.numel()
+    if copy_row.numel() != n or n == 0:
+        _fail("copy_row must have one entry per copy")
+    dev = token_of_copy.device
+    offsets = torch.empty(num_tokens + 1, dtype=torch.int32, device=dev)
+    copies = torch.empty(n, dtype=torch.int32, device=dev)
+    check(lib().sb_token_csr(token_of_copy.data_ptr(), 1 if token_of_copy.dtype == torch.int64 else 0,
+                             copy_row.data_ptr(), n, num_tokens, offsets.data_ptr(), copies.data_ptr(),
+                             stream_of(dev)))
+    return offsets, copies
+
+
+def combine_assigned_cuda(
+    y: torch.Tensor,
+    copy_row: torch.Tensor,
+    weight_of_copy: torch.Tensor,
+    token_offsets: torch.Tensor,
+    token_copies: torch.Tensor | None,
+    num_tokens: int,
+    valid_tokens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """out [T, D] bf16: out[t] = sum over t's copies c (token_copies[token_offsets[t]:
+    token_offsets[t+1]], or c = the index itself when token_copies is None) of
+    fp32(y[copy_row[c]]) * fp32(weight_of_copy[c]), fp32 sum in copy order; 0 for
+    a token with no copy."""
+    if not (y.is_cuda and copy_row.is_cuda and weight_of_copy.is_cuda):
+        _fail("y, copy_row and weight_of_copy must be CUDA tensors")
+    if y.dtype != torch.bfloat16 or y.dim() != 2 or not y.is_contiguous():
+        _fail(f"y must be a contiguous [rows, D] bfloat16 tensor, got {_shape(y)} {y.dtype}")
+    _check_index(copy_row, "copy_row")
+    _check_index(token_offsets, "token_offsets")
+    if token_copies is not None:
+        _check_index(token_copies, "token_copies")
+    if token_offsets.numel() != num_tokens + 1:
+        _fail(f"token_offsets must have T+1 = {num_tokens + 1} entries, got {token_offsets.numel()}")
+    if weight_of_copy.dim() != 1 or weight_of_copy.numel() < copy_row.numel():
+        _fail("weight_of_copy must be 1-D with one entry per copy")
+    weights = weight_of_copy if weight_of_copy.dtype in _GATE_DTYPES else weight_of_copy.float()
+    weights = weights.contiguous()
+    out = torch.empty(num_tokens, y.shape[1], dtype=y.dtype, device=y.device)
+    if num_tokens == 0:
+        return out
+    check(lib().sb_combine_assigned(
+        y.data_ptr(), copy_row.data_ptr(), weights.data_ptr(), _GATE_DTYPES[weights.dtype], token_offsets.data_ptr(),
+        _ptr(token_copies), out.data_ptr(), num_tokens, y.shape[1], y.shape[0], _ptr(valid_tokens),
+        stream_of(y.device),
+    ))
+    return out
+
+
+def _check_scores(scores: torch.Tensor) -> None:
+    if not (scores.is_cuda and scores.dtype == torch.float32 and scores.dim() == 2 and scores.is_contiguous()):
+        _fail("scores must be a contiguous [T, E] float32 CUDA tensor")
+    if scores.shape[0] == 0 or scores.shape[1] == 0:
+        _fail(f"scores must be [T, E] with T, E > 0, got {_shape(scores)}")
+
+
+def router_topk_cuda(scores: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(top_idx [T, k] int32, top_weight [T, k] fp32): the k best experts of each
+    token, best first (equal scores: lower expert first), and the picked
+    scores over their sum."""
+    _check_scores(scores)
+    num_tokens, num_experts = scores.shape
+    idx = torch.empty(num_tokens, k, dtype=torch.int32, device=scores.device)
+    weight = torch.empty(num_tokens, k, dtype=torch.float32, device=scores.device)
+    check(lib().sb_router_topk(scores.data_ptr(), num_tokens, num_experts, k, idx.data_ptr(), weight.data_ptr(),
+                               stream_of(scores.device)))
+    return idx, weight
+
+
+def router_sizes(num_tokens: int, num_experts: int, k: int, tile: int, block_size: int, ffn_dim: int
+                 ) -> tuple[int, int, int, int]:
+    """(list capacity, max_row_blocks, max_rows, workspace int32 elements) of token rounding."""
+    cap, rb, rows, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    check(lib().sb_router_sizes(num_tokens, num_experts, k, tile, block_size, ffn_dim, ctypes.byref(cap),
+                                ctypes.byref(rb), ctypes.byref(rows), ctypes.byref(ws)))
+    return cap.value, rb.value, rows.value, ws.value
+
+
+def token_rounding_cuda(scores: torch.Tensor, k: int, tile: int, ffn_dim: int, block_size: int
+                        ) -> dict[str, torch.Tensor]:
+    """Token rounding fused with routing, no host sync. Returns the list
+    (token_of_copy / expert_of_copy int32, weight_of_copy fp32, capacity-sized,
+    -1 / -1 / 0 past the end), num_assignments [1], token_offsets [T+1], and the
+    8 routing outputs of build_topology_assigned_cuda for that list."""
+    _check_scores(scores)
+    num_tokens, num_experts = scores.shape
+    cap, max_row_blocks, max_rows, ws = router_sizes(num_tokens, num_experts, k, tile, block_size, ffn_dim)
+    dev = scores.device
+    i32 = {"dtype": torch.int32, "device": dev}
+    out = {
+        "token_of_copy": torch.empty(cap, **i32),
+        "expert_of_copy": torch.empty(cap, **i32),
+        "weight_of_copy": torch.empty(cap, dtype=torch.float32, device=dev),
+        "num_assignments": torch.empty(1, **i32),
+        "token_offsets": torch.empty(num_tokens + 1, **i32),
+        "tokens_per_expert": torch.empty(num_experts, **i32),
+        "padded_offsets": torch.empty(num_experts + 1, **i32),
+        "row_token": torch.empty(max_rows, **i32),
+        "copy_row": torch.empty(cap, **i32),
+        "row_block_expert": torch.empty(max_row_blocks, **i32),
+        "row_offsets": torch.empty(max_row_blocks + 1, **i32),
+        "col_indices": torch.empty(max_row_blocks * (ffn_dim // block_size), **i32),
+        "error": torch.empty(1, **i32),
+    }
+    workspace = torch.empty(ws, **i32)
+    check(lib().sb_token_rounding(
+        scores.data_ptr(), num_tokens, num_experts, k, tile, block_size, ffn_dim, workspace.data_ptr(),
+        *(t.data_ptr() for t in out.values()), stream_of(dev),
+    ))
+    return out

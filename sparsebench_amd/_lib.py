@@ -37,6 +37,24 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sb_sdd": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]),
     "sb_dsd": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]),
     "sb_combine": (_c_int, [_ptr, _ptr, _ptr, _i32, _ptr, _i64, _i32, _i64, _i64, _ptr, _ptr]),
+    "sb_routing_assigned": (
+        _c_int,
+        [_ptr, _i32, _ptr, _i32, _i64, _i64, _i32, _i32, _i32, _ptr, _ptr,
+         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
+    ),
+    "sb_token_csr": (_c_int, [_ptr, _i32, _ptr, _i64, _i64, _ptr, _ptr, _ptr]),
+    "sb_combine_assigned": (_c_int, [_ptr, _ptr, _ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr]),
+    "sb_router_sizes": (
+        _c_int,
+        [_i64, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+         ctypes.POINTER(_i64)],
+    ),
+    "sb_router_topk": (_c_int, [_ptr, _i64, _i32, _i32, _ptr, _ptr, _ptr]),
+    "sb_token_rounding": (
+        _c_int,
+        [_ptr, _i64, _i32, _i32, _i32, _i32, _i32, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
+    ),
 }
 
 SB_OK = 0

@@ -18,13 +18,13 @@
 // Place's two roles touch disjoint memory and depend only on step 2.
 
 #include "common.hpp"
+#include "layout.hpp"
 
 namespace sb {
 namespace {
 
 constexpr int kChunk = 1024;             // copies per count/place workgroup, one per lane
 constexpr int kWaves = kChunk / 64;      // 16 wave64s
-constexpr int kMaxExperts = 1024;
 constexpr int kLayoutItemsPerGroup = 1024;
 
 __device__ __forceinline__ uint64_t lanes_below() {
@@ -44,22 +44,48 @@ __device__ __forceinline__ uint64_t same_expert_lanes(bool valid, int32_t e, int
   return peers;
 }
 
-template <typename Idx>
-__device__ __forceinline__ int32_t read_expert(const Idx* __restrict__ idx, int64_t c, int64_t n, int32_t k,
-                                               int32_t num_experts, const int32_t* __restrict__ valid_tokens,
-                                               bool* bad) {
+// Where copy c's token comes from: c / k for top-k routing, or a list of
+// token ids (one per copy) for a routing given as assignments.
+template <typename Tok>
+struct TokenSource {
+  const Tok* __restrict__ ids;  // nullptr: token = c / k
+  int32_t k;
+  int64_t num_tokens;
+  __device__ __forceinline__ int64_t token(int64_t c) const {
+    return ids != nullptr ? static_cast<int64_t>(ids[c]) : c / k;
+  }
+};
+
+// Expert of copy c, or -1 when the copy is skipped. A copy past the end or
+// of a token >= *valid_tokens is skipped silently; a bad expert id (or a
+// token id outside [0, T)) is skipped and reported through *bad.
+template <typename Idx, typename Tok>
+__device__ __forceinline__ int32_t read_expert(const Idx* __restrict__ idx, int64_t c, int64_t n,
+                                               const TokenSource<Tok>& src, int32_t num_experts,
+                                               const int32_t* __restrict__ valid_tokens, bool* bad,
+                                               int32_t* token) {
   *bad = false;
+  *token = -1;
   if (c >= n) return -1;
-  if (valid_tokens != nullptr && c / k >= static_cast<int64_t>(*valid_tokens)) return -1;
+  const int64_t t = src.token(c);
+  if (t < 0 || t >= src.num_tokens) {
+    *bad = true;
+    return -1;
+  }
+  if (valid_tokens != nullptr && t >= static_cast<int64_t>(*valid_tokens)) return -1;
   const Idx v = idx[c];
-  if (v >= 0 && v < static_cast<Idx>(num_experts)) return static_cast<int32_t>(v);
+  if (v >= 0 && v < static_cast<Idx>(num_experts)) {
+    *token = static_cast<int32_t>(t);
+    return static_cast<int32_t>(v);
+  }
   *bad = true;
   return -1;
 }
 
-template <typename Idx>
-__global__ void __launch_bounds__(kChunk) route_count_kernel(const Idx* __restrict__ idx, int64_t n, int32_t k,
-                                                             int32_t num_experts, int32_t num_bits,
+template <typename Idx, typename Tok>
+__global__ void __launch_bounds__(kChunk) route_count_kernel(const Idx* __restrict__ idx, int64_t n,
+                                                             TokenSource<Tok> tokens, int32_t num_experts,
+                                                             int32_t num_bits,
                                                              const int32_t* __restrict__ valid_tokens,
                                                              int32_t* __restrict__ counts) {
   __shared__ int32_t hist[kMaxExperts + 1];
@@ -69,7 +95,8 @@ __global__ void __launch_bounds__(kChunk) route_count_kernel(const Idx* __restri
 
   const int64_t c = static_cast<int64_t>(blockIdx.x) * kChunk + tid;
   bool bad;
-  const int32_t e = read_expert(idx, c, n, k, num_experts, valid_tokens, &bad);
+  int32_t token;
+  const int32_t e = read_expert(idx, c, n, tokens, num_experts, valid_tokens, &bad, &token);
   const bool valid = e >= 0;
   // One LDS add per distinct expert in the wave instead of one per copy:
   // skewed routing would otherwise serialize 64 adds on one address.
@@ -147,9 +174,10 @@ __global__ void __launch_bounds__(kChunk) route_offsets_kernel(int32_t* __restri
   if (tid == 0) padded_offsets[0] = 0;
 }
 
-template <typename Idx>
+template <typename Idx, typename Tok>
 __global__ void __launch_bounds__(kChunk)
-    route_place_kernel(const Idx* __restrict__ idx, int64_t n, int32_t k, int32_t num_experts, int32_t num_bits,
+    route_place_kernel(const Idx* __restrict__ idx, int64_t n, TokenSource<Tok> tokens, int32_t num_experts,
+                       int32_t num_bits,
                        const int32_t* __restrict__ valid_tokens, int32_t num_chunks,
                        const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ tokens_per_expert,
                        const int32_t* __restrict__ padded_offsets, int32_t block_size, int32_t ffn_blocks,
@@ -168,7 +196,8 @@ __global__ void __launch_bounds__(kChunk)
 
     const int64_t c = static_cast<int64_t>(blockIdx.x) * kChunk + tid;
     bool bad;
-    const int32_t e = read_expert(idx, c, n, k, num_experts, valid_tokens, &bad);
+    int32_t token;
+    const int32_t e = read_expert(idx, c, n, tokens, num_experts, valid_tokens, &bad, &token);
     const bool valid = e >= 0;
     const uint64_t peers = same_expert_lanes(valid, e, num_bits);
     const uint64_t lower = peers & lanes_below();
@@ -183,7 +212,7 @@ __global__ void __launch_bounds__(kChunk)
                           chunk_base[static_cast<int64_t>(blockIdx.x) * (num_experts + 1) + e] + before +
                           __popcll(lower);
       copy_row[c] = row;
-      row_token[row] = static_cast<int32_t>(c / k);
+      row_token[row] = token;
     } else if (c < n) {
       copy_row[c] = -1;
     }
@@ -196,42 +225,9 @@ __global__ void __launch_bounds__(kChunk)
   for (int e = tid; e <= num_experts; e += kChunk) offs[e] = padded_offsets[e];
   for (int e = tid; e < num_experts; e += kChunk) cnts[e] = tokens_per_expert[e];
   __syncthreads();
-
-  const int32_t num_rows = offs[num_experts];
-  const int32_t num_row_blocks = num_rows / block_size;
-  // Last expert whose range starts at or before `row`: empty experts share a
-  // start with the next one, and "last" steps over them.
-  auto expert_of_row = [&](int32_t row) {
-    int32_t lo = 0, hi = num_experts - 1;
-    while (lo < hi) {
-      const int32_t mid = (lo + hi + 1) >> 1;
-      if (offs[mid] <= row) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-  };
-
   const int64_t i = static_cast<int64_t>(blockIdx.x - num_chunks) * kLayoutItemsPerGroup + tid;
-  const int64_t bsr_items = static_cast<int64_t>(max_row_blocks) * ffn_blocks;
-  if (i <= max_row_blocks) {
-    const int32_t r = static_cast<int32_t>(i);
-    row_offsets[r] = (r < num_row_blocks ? r : num_row_blocks) * ffn_blocks;
-  }
-  if (i < bsr_items) {
-    const int32_t r = static_cast<int32_t>(i / ffn_blocks);
-    const int32_t j = static_cast<int32_t>(i % ffn_blocks);
-    const int32_t expert = r < num_row_blocks ? expert_of_row(r * block_size) : -1;
-    col_indices[i] = expert < 0 ? -1 : expert * ffn_blocks + j;
-    if (j == 0) row_block_expert[r] = expert;
-  }
-  if (i < max_rows) {
-    const int32_t row = static_cast<int32_t>(i);
-    bool copy_here = false;
-    if (row < num_rows) {
-      const int32_t e = expert_of_row(row);
-      copy_here = row - offs[e] < cnts[e];
-    }
-    if (!copy_here) row_token[row] = -1;
-  }
+  layout_item(i, offs, cnts, num_experts, block_size, ffn_blocks, max_row_blocks, max_rows, row_token,
+              row_block_expert, row_offsets, col_indices);
 }
 
 int bits_for(int32_t num_experts) {
@@ -267,6 +263,39 @@ extern "C" int sb_routing_sizes(int64_t num_copies, int32_t num_experts, int32_t
   return clear_ok();
 }
 
+namespace sb {
+namespace {
+
+// The three routing launches for n copies whose tokens come from `tokens`.
+template <typename Idx, typename Tok>
+int launch_routing(const Idx* idx, int64_t n, TokenSource<Tok> tokens, int32_t num_experts, int32_t ffn_dim,
+                   int32_t block_size, const int32_t* valid_tokens, int32_t* workspace, int32_t* tokens_per_expert,
+                   int32_t* padded_offsets, int32_t* row_token, int32_t* copy_row, int32_t* row_block_expert,
+                   int32_t* row_offsets, int32_t* col_indices, int32_t* error, hipStream_t stream) {
+  int64_t max_row_blocks = 0, max_rows = 0, ws = 0;
+  if (int rc = sb_routing_sizes(n, num_experts, ffn_dim, block_size, &max_row_blocks, &max_rows, &ws)) return rc;
+  const int32_t num_chunks = static_cast<int32_t>((n + kChunk - 1) / kChunk);
+  const int32_t ffn_blocks = ffn_dim / block_size;
+  const int num_bits = bits_for(num_experts);
+  const int64_t layout_items = std::max<int64_t>(max_row_blocks * ffn_blocks + 1, max_rows);
+  const int32_t layout_groups = static_cast<int32_t>((layout_items + kLayoutItemsPerGroup - 1) / kLayoutItemsPerGroup);
+
+  route_count_kernel<Idx, Tok><<<num_chunks, kChunk, 0, stream>>>(idx, n, tokens, num_experts, num_bits,
+                                                                  valid_tokens, workspace);
+  if (int rc = check_launch("routing count")) return rc;
+  route_offsets_kernel<<<1, kChunk, 0, stream>>>(workspace, num_chunks, num_experts, block_size, tokens_per_expert,
+                                                 padded_offsets, error);
+  if (int rc = check_launch("routing offsets")) return rc;
+  route_place_kernel<Idx, Tok><<<num_chunks + layout_groups, kChunk, 0, stream>>>(
+      idx, n, tokens, num_experts, num_bits, valid_tokens, num_chunks, workspace, tokens_per_expert, padded_offsets,
+      block_size, ffn_blocks, static_cast<int32_t>(max_row_blocks), max_rows, copy_row, row_token, row_block_expert,
+      row_offsets, col_indices);
+  return check_launch("routing place");
+}
+
+}  // namespace
+}  // namespace sb
+
 extern "C" int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, int32_t k,
                           int32_t num_experts, int32_t ffn_dim, int32_t block_size, const int32_t* valid_tokens,
                           int32_t* workspace, int32_t* tokens_per_expert, int32_t* padded_offsets,
@@ -279,39 +308,45 @@ extern "C" int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t nu
   if (!expert_idx || !workspace || !tokens_per_expert || !padded_offsets || !row_token || !copy_row ||
       !row_block_expert || !row_offsets || !col_indices || !error)
     return fail(SB_ERR_INVALID, "sb_routing: null buffer");
-
+  const TokenSource<int32_t> tokens{nullptr, k, num_tokens};
   const hipStream_t stream = as_stream(stream_ptr);
-  const int32_t num_chunks = static_cast<int32_t>((n + kChunk - 1) / kChunk);
-  const int32_t ffn_blocks = ffn_dim / block_size;
-  const int num_bits = bits_for(num_experts);
-  const int64_t layout_items = std::max<int64_t>(max_row_blocks * ffn_blocks + 1, max_rows);
-  const int32_t layout_groups = static_cast<int32_t>((layout_items + kLayoutItemsPerGroup - 1) / kLayoutItemsPerGroup);
+  const int rc = idx_is_i64
+                     ? launch_routing(static_cast<const int64_t*>(expert_idx), n, tokens, num_experts, ffn_dim,
+                                      block_size, valid_tokens, workspace, tokens_per_expert, padded_offsets,
+                                      row_token, copy_row, row_block_expert, row_offsets, col_indices, error, stream)
+                     : launch_routing(static_cast<const int32_t*>(expert_idx), n, tokens, num_experts, ffn_dim,
+                                      block_size, valid_tokens, workspace, tokens_per_expert, padded_offsets,
+                                      row_token, copy_row, row_block_expert, row_offsets, col_indices, error, stream);
+  return rc ? rc : clear_ok();
+}
 
-  if (idx_is_i64) {
-    route_count_kernel<int64_t><<<num_chunks, kChunk, 0, stream>>>(
-        static_cast<const int64_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, workspace);
-  } else {
-    route_count_kernel<int32_t><<<num_chunks, kChunk, 0, stream>>>(
-        static_cast<const int32_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, workspace);
-  }
-  if (int rc = check_launch("routing count")) return rc;
-
-  route_offsets_kernel<<<1, kChunk, 0, stream>>>(workspace, num_chunks, num_experts, block_size, tokens_per_expert,
-                                                 padded_offsets, error);
-  if (int rc = check_launch("routing offsets")) return rc;
-
-  const int32_t grid = num_chunks + layout_groups;
-  if (idx_is_i64) {
-    route_place_kernel<int64_t><<<grid, kChunk, 0, stream>>>(
-        static_cast<const int64_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, num_chunks, workspace,
-        tokens_per_expert, padded_offsets, block_size, ffn_blocks, static_cast<int32_t>(max_row_blocks), max_rows,
-        copy_row, row_token, row_block_expert, row_offsets, col_indices);
-  } else {
-    route_place_kernel<int32_t><<<grid, kChunk, 0, stream>>>(
-        static_cast<const int32_t*>(expert_idx), n, k, num_experts, num_bits, valid_tokens, num_chunks, workspace,
-        tokens_per_expert, padded_offsets, block_size, ffn_blocks, static_cast<int32_t>(max_row_blocks), max_rows,
-        copy_row, row_token, row_block_expert, row_offsets, col_indices);
-  }
-  if (int rc = check_launch("routing place")) return rc;
-  return clear_ok();
+extern "C" int sb_routing_assigned(const void* expert_of_copy, int32_t expert_is_i64, const void* token_of_copy,
+                                   int32_t token_is_i64, int64_t num_copies, int64_t num_tokens, int32_t num_experts,
+                                   int32_t ffn_dim, int32_t block_size, const int32_t* valid_tokens,
+                                   int32_t* workspace, int32_t* tokens_per_expert, int32_t* padded_offsets,
+                                   int32_t* row_token, int32_t* copy_row, int32_t* row_block_expert,
+                                   int32_t* row_offsets, int32_t* col_indices, int32_t* error, void* stream_ptr) {
+  if (num_copies <= 0) return fail(SB_ERR_INVALID, "routing: the assignment list must not be empty");
+  if (num_tokens <= 0 || num_tokens > 2147483647LL) return fail(SB_ERR_INVALID, "routing: bad token count");
+  int64_t max_row_blocks = 0, max_rows = 0, ws = 0;
+  if (int rc = sb_routing_sizes(num_copies, num_experts, ffn_dim, block_size, &max_row_blocks, &max_rows, &ws))
+    return rc;
+  if (!expert_of_copy || !token_of_copy || !workspace || !tokens_per_expert || !padded_offsets || !row_token ||
+      !copy_row || !row_block_expert || !row_offsets || !col_indices || !error)
+    return fail(SB_ERR_INVALID, "sb_routing_assigned: null buffer");
+  const hipStream_t stream = as_stream(stream_ptr);
+  auto run = [&](auto tok_ptr) {
+    using Tok = std::remove_cv_t<std::remove_pointer_t<decltype(tok_ptr)>>;
+    const TokenSource<Tok> tokens{tok_ptr, 1, num_tokens};
+    return expert_is_i64
+               ? launch_routing(static_cast<const int64_t*>(expert_of_copy), num_copies, tokens, num_experts,
+                                ffn_dim, block_size, valid_tokens, workspace, tokens_per_expert, padded_offsets,
+                                row_token, copy_row, row_block_expert, row_offsets, col_indices, error, stream)
+               : launch_routing(static_cast<const int32_t*>(expert_of_copy), num_copies, tokens, num_experts,
+                                ffn_dim, block_size, valid_tokens, workspace, tokens_per_expert, padded_offsets,
+                                row_token, copy_row, row_block_expert, row_offsets, col_indices, error, stream);
+  };
+  const int rc = token_is_i64 ? run(static_cast<const int64_t*>(token_of_copy))
+                              : run(static_cast<const int32_t*>(token_of_copy));
+  return rc ? rc : clear_ok();
 }

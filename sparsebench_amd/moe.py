@@ -14,7 +14,7 @@ from collections.abc import Callable
 
 import torch
 
-from sparsebench_amd.routing import route_device
+from sparsebench_amd.routing import AssignedRouting, route_assigned, route_device, route_rounded
 from sparsebench_amd.spmm import dsd, sdd
 
 BLOCK_SIZE = 128
@@ -67,3 +67,78 @@ def moe_forward(
     out = combine(y, topo.copy_row, expert_weight, valid_tokens)
     mark("combine")
     return out
+
+
+def _assigned_layer(x, routing: AssignedRouting, weight_of_copy, w1, w2, mark, valid_tokens) -> torch.Tensor:
+    from sparsebench_amd import _C
+
+    num_experts, d_model, ffn_dim = w1.shape
+    mark("routing")
+    h = sdd(x, w1, routing.topology, gelu=True)
+    mark("SDD + GELU (fused)")
+    y = dsd(h, w2.view(num_experts * ffn_dim, d_model), routing.topology, version=5)
+    mark("DSD")
+    out = _C.combine_assigned_cuda(y, routing.topology.copy_row, weight_of_copy, routing.token_offsets,
+                                   routing.token_copies, x.shape[0], valid_tokens)
+    mark("combine")
+    return out
+
+
+def moe_forward_assigned(
+    x: torch.Tensor,
+    token_of_copy: torch.Tensor,
+    expert_of_copy: torch.Tensor,
+    weight_of_copy: torch.Tensor,
+    w1: torch.Tensor,
+    w2: torch.Tensor,
+    mark: Callable[[str], None] = _no_mark,
+    valid_tokens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The same layer for any routing given as a flat list (the reference's
+    sparsebench/moe.py:59-91): copy c sends token_of_copy[c] to
+    expert_of_copy[c] with weight weight_of_copy[c]. A token may have any
+    number of copies, including none (its output row is 0), e.g. after token
+    rounding. No host sync.
+
+    The routing is moe_forward's with k = 1 and token ids from the list. The
+    combine sums each token's copies in list order with fp32 accumulation,
+    as the reference's index_add_ does on the CPU (on the GPU its order is not
+    fixed), so the same list always gives the same bits, and a top-k list
+    gives exactly moe_forward's result. A token id outside [0, T) is skipped
+    and flagged in the routing's error word.
+    """
+    num_experts, d_model, ffn_dim = w1.shape
+    if w2.shape != (num_experts, ffn_dim, d_model):
+        raise ValueError(f"w2 must be {(num_experts, ffn_dim, d_model)}, got {tuple(w2.shape)}")
+    if x.dim() != 2 or x.shape[1] != d_model:
+        raise ValueError(f"x must be [T, {d_model}], got {tuple(x.shape)}")
+    n = expert_of_copy.numel()
+    if token_of_copy.numel() != n or weight_of_copy.numel() != n:
+        raise ValueError("token_of_copy, expert_of_copy and weight_of_copy must have one entry per copy")
+    if n == 0:  # host-known size: nothing routed anywhere
+        return torch.zeros_like(x)
+    routing = route_assigned(token_of_copy.reshape(-1), expert_of_copy.reshape(-1), x.shape[0], num_experts,
+                             ffn_dim, BLOCK_SIZE, valid_tokens)
+    return _assigned_layer(x, routing, weight_of_copy.reshape(-1), w1, w2, mark, valid_tokens)
+
+
+def moe_forward_rounded(
+    x: torch.Tensor,
+    scores: torch.Tensor,
+    k: int,
+    w1: torch.Tensor,
+    w2: torch.Tensor,
+    tile: int = BLOCK_SIZE,
+    mark: Callable[[str], None] = _no_mark,
+) -> torch.Tensor:
+    """The layer with token rounding fused into routing, no host sync:
+    moe_forward_assigned(x, *token_rounding(scores, k, tile), w1, w2) without
+    the sync token_rounding needs for its length. scores [T, E] fp32 router
+    probabilities. Bit-identical to that two-step form."""
+    num_experts, d_model, ffn_dim = w1.shape
+    if w2.shape != (num_experts, ffn_dim, d_model):
+        raise ValueError(f"w2 must be {(num_experts, ffn_dim, d_model)}, got {tuple(w2.shape)}")
+    if x.dim() != 2 or x.shape[1] != d_model or scores.shape != (x.shape[0], num_experts):
+        raise ValueError(f"x must be [T, {d_model}] and scores [T, {num_experts}]")
+    routing = route_rounded(scores, k, ffn_dim, BLOCK_SIZE, tile)
+    return _assigned_layer(x, routing, routing.weight_of_copy, w1, w2, mark, None)

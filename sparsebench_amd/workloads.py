@@ -47,6 +47,21 @@ def routing_case(name: str, num_tokens: int, num_experts: int, seed: int = 0, k:
     raise ValueError(name)
 
 
+def router_scores(name: str, num_tokens: int, num_experts: int, seed: int = 0) -> torch.Tensor:
+    """Softmax router scores [T, E] fp32 on the CPU, for routers that need full
+    scores (token rounding), drawn with the same generator calls as the
+    reference (sparsebench/workloads.py:39-52): "uniform" = N(0, 1) logits;
+    "zipf" adds -1.2 log(rank) per expert, so popularity falls off like
+    routing_case("zipf")."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(num_tokens, num_experts, generator=g)
+    if name == "zipf":
+        logits = logits - ZIPF_EXPONENT * torch.log(torch.arange(1, num_experts + 1, dtype=torch.float32))
+    elif name != "uniform":
+        raise ValueError(name)
+    return torch.softmax(logits, dim=-1)
+
+
 def softmax_gates(num_tokens: int, k: int, seed: int, device: str | torch.device = "cpu") -> torch.Tensor:
     """[T, k] gate weights: softmax over the k picks of N(0, 1) logits (fp32)."""
     g = torch.Generator().manual_seed(seed)

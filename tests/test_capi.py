@@ -112,3 +112,50 @@ def test_combine_rejects_gate_dtype(lib) -> None:
     p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
     assert lib.sb_combine(p, p, p, 7, p, 1, 2, 8, 4, None, None) == 1
     assert "gate dtype" in _err(lib)
+
+
+@pytest.mark.parametrize(("num_tokens", "num_experts", "k", "tile"),
+                         [(4096, 64, 2, 128), (50, 3, 1, 4), (16384, 128, 2, 128), (1000, 65, 3, 16)])
+def test_router_sizes(lib, num_tokens: int, num_experts: int, k: int, tile: int) -> None:
+    cap, rb, rows, ws = (ctypes.c_int64() for _ in range(4))
+    rc = lib.sb_router_sizes(num_tokens, num_experts, k, tile, 128, 512, ctypes.byref(cap), ctypes.byref(rb),
+                             ctypes.byref(rows), ctypes.byref(ws))
+    assert rc == 0, _err(lib)
+    # An expert rounds up by less than half a tile; never more than T*E assignments.
+    assert cap.value == min(num_tokens * num_experts, num_tokens * k + num_experts * (tile // 2))
+    assert (rb.value, rows.value) == worst_case_sizes(cap.value, num_experts, 512, 128)
+    words, chunks = (num_tokens + 31) // 32, (num_tokens + 63) // 64
+    assert ws.value == chunks * num_experts + num_experts + num_tokens * num_experts + 2 * words * num_experts \
+        + 2 * num_tokens
+
+
+@pytest.mark.parametrize(("args", "match"), [
+    ((0, 8, 2, 128), "T > 0"), ((10, 0, 2, 128), "num_experts"), ((10, 2000, 2, 128), "num_experts"),
+    ((10, 8, 0, 128), "k must be"), ((10, 8, 9, 128), "k must be"), ((100, 64, 17, 128), "k must be"),
+    ((10, 8, 2, 0), "tile"),
+])
+def test_router_sizes_reject(lib, args, match: str) -> None:
+    assert lib.sb_router_sizes(*args, 128, 256, None, None, None, None) == 1
+    assert match in _err(lib)
+
+
+def test_router_entry_points_reject_null_buffers(lib) -> None:
+    assert lib.sb_router_topk(None, 10, 8, 2, None, None, None) == 1
+    assert "null buffer" in _err(lib)
+    assert lib.sb_token_rounding(None, 10, 8, 2, 128, 128, 256, *([None] * 15)) == 1
+    assert "null buffer" in _err(lib)
+
+
+def test_assigned_entry_points_reject(lib) -> None:
+    assert lib.sb_routing_assigned(None, 0, None, 0, 0, 10, 8, 256, 128, None, *([None] * 10)) == 1
+    assert "must not be empty" in _err(lib)
+    assert lib.sb_routing_assigned(None, 0, None, 0, 5, 10, 8, 256, 128, None, *([None] * 10)) == 1
+    assert "null buffer" in _err(lib)
+    assert lib.sb_token_csr(None, 0, None, 5, 0, None, None, None) == 1
+    assert "token count" in _err(lib)
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
+    assert lib.sb_combine_assigned(p, p, p, 9, p, None, p, 1, 8, 4, None, None) == 1
+    assert "weight dtype" in _err(lib)
+    assert lib.sb_combine_assigned(p, p, p, 2, p, None, p, 1, 12, 4, None, None) == 1
+    assert "multiple of 8" in _err(lib)

@@ -10,15 +10,19 @@ import torch
 
 def test_package_aliases_as_sparsebench() -> None:
     import sparsebench_amd
-    from sparsebench_amd import _C, moe, routing, spmm, topology, workloads
+    from sparsebench_amd import _C, moe, routing, spmm, token_rounding, topology, workloads
 
     saved = {k: v for k, v in sys.modules.items() if k == "sparsebench" or k.startswith("sparsebench.")}
     try:
         for name, mod in {"": sparsebench_amd, "._C": _C, ".moe": moe, ".routing": routing, ".spmm": spmm,
-                          ".topology": topology, ".workloads": workloads}.items():
+                          ".token_rounding": token_rounding, ".topology": topology,
+                          ".workloads": workloads}.items():
             sys.modules["sparsebench" + name] = mod
-        from sparsebench.moe import moe_forward  # noqa: F401  (the reference's import line)
+        from sparsebench.moe import moe_forward, moe_forward_assigned  # noqa: F401  (the reference's imports)
         from sparsebench.routing import DeviceTopology, route_device  # noqa: F401
+        from sparsebench.token_rounding import (  # noqa: F401
+            Assignments, round_counts, routing_change, token_rounding, top_k_assignments)
+        from sparsebench.workloads import router_scores  # noqa: F401
         from sparsebench import _C as c
 
         assert {"arch_probe", "build_topology_cuda", "sdd_cuda", "dsd_cuda"} <= set(dir(c))
@@ -86,3 +90,56 @@ def test_workload_shapes_and_flops() -> None:
     # Zipf over a permutation: the hottest expert is not expert 0 for this seed, and counts are skewed.
     counts = torch.bincount(idx.flatten(), minlength=64)
     assert int(counts.max()) > 4 * int(counts.float().median())
+
+
+def test_assignments_fields_match_the_reference() -> None:
+    from sparsebench_amd.token_rounding import Assignments
+
+    assert [f.name for f in dataclasses.fields(Assignments)] == ["token", "expert", "weight"]
+
+
+def test_round_counts_nearest_ties_down() -> None:
+    # tests/test_token_rounding.py:12-15 (reference): host arithmetic on a few counts
+    from sparsebench_amd.token_rounding import round_counts
+
+    counts = torch.tensor([0, 1, 63, 64, 65, 128, 191, 192, 200])
+    expected = torch.tensor([0, 0, 0, 0, 128, 128, 128, 128, 256])
+    assert torch.equal(round_counts(counts, 128, 10_000), expected)
+
+
+def test_router_scores_match_the_reference_recipe() -> None:
+    from sparsebench_amd.workloads import router_scores
+
+    s = router_scores("zipf", 100, 8)
+    assert s.shape == (100, 8) and s.dtype == torch.float32
+    torch.testing.assert_close(s.sum(dim=1), torch.ones(100))
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(100, 8, generator=g) - 1.2 * torch.log(torch.arange(1, 9, dtype=torch.float32))
+    assert torch.equal(s, torch.softmax(logits, dim=-1))
+    with pytest.raises(ValueError):
+        router_scores("skewed", 4, 4)
+
+
+def test_moe_forward_assigned_rejects_bad_lists_before_the_gpu() -> None:
+    from sparsebench_amd.moe import moe_forward_assigned
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w1 = torch.zeros(2, 64, 256, dtype=torch.bfloat16)
+    w2 = torch.zeros(2, 256, 64, dtype=torch.bfloat16)
+    t = torch.zeros(3, dtype=torch.long)
+    with pytest.raises(ValueError, match="one entry per copy"):
+        moe_forward_assigned(x, t, t, torch.ones(2), w1, w2)
+    with pytest.raises(ValueError, match="w2"):
+        moe_forward_assigned(x, t, t, torch.ones(3), w1, w1)
+    # An empty list is answered on the host, like the reference (moe.py:76-77).
+    e = torch.zeros(0, dtype=torch.long)
+    assert torch.equal(moe_forward_assigned(x, e, e, torch.ones(0), w1, w2), torch.zeros_like(x))
+
+
+def test_router_rejects_cpu_scores() -> None:
+    from sparsebench_amd.token_rounding import token_rounding, top_k_assignments
+
+    with pytest.raises(RuntimeError, match="CUDA"):
+        token_rounding(torch.rand(10, 4), 2)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        top_k_assignments(torch.rand(10, 4), 2)

@@ -1,0 +1,212 @@
+"""Same-box comparison tables: this build's MoE layer against other ways of
+computing it on the same MI355X (the measurements of the reference's
+bench/bench_moe.py and bench/bench_token_rounding.py, made here).
+
+    python bench_baselines.py                 # both tables, markdown on stdout
+    python bench_baselines.py --only layer    # or: --only rounding
+
+Layer pipelines (everything from the routing to the [T, D] output is timed,
+host syncs included):
+  ours          moe_forward: GPU routing -> SDD (+ gather, GELU) -> DSD -> combine;
+                no host sync. Timed eagerly, and as a captured graph.
+  grouped_mm    sort copies by expert -> torch._grouped_mm -> GELU ->
+                torch._grouped_mm -> unsort -> weighted sum (torch ops, no sync).
+  loop          per expert: x[tokens] @ w1[e] -> GELU -> @ w2[e], expert counts
+                read on the host (syncs).
+
+Token rounding (SonicMoE; the router's scores from workloads.router_scores):
+  the layer on the plain top-k list and on the token-rounded list, for
+  moe_forward_assigned and for the grouped_mm pipeline on the same list; the
+  rounding step alone (routing.route_rounded: rounding, its list and its
+  layout, no sync); and moe_forward_rounded (rounding fused into the layer).
+
+Every pipeline is checked against the fp32 loop reference before it is
+timed (max error <= 3e-2 (1 + max |ref|), the reference's check). Timing: a
+512 MiB buffer is zeroed before each step (outside the events), events on
+the current stream, median of 20 after 3 warm-ups.
+"""
+
+from __future__ import annotations
+
+import argparse
+import statistics
+
+import torch
+import torch.nn.functional as F
+
+from sparsebench_amd.moe import moe_forward, moe_forward_assigned, moe_forward_rounded
+from sparsebench_amd.routing import route_rounded
+from sparsebench_amd.token_rounding import token_rounding, top_k_assignments
+from sparsebench_amd.workloads import SHAPES, make_layer, router_scores
+
+TOL = 3e-2
+FLUSH_BYTES = 512 << 20
+
+
+def time_ms(fn, flush: torch.Tensor, steps: int = 20, warmup: int = 3) -> float:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(steps):
+        flush.zero_()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times)
+
+
+def reference_fp32(x, token, expert, weight, w1, w2) -> torch.Tensor:
+    """Loop over experts in fp32 on the GPU (ground truth for the checks)."""
+    out = torch.zeros(x.shape[0], x.shape[1], device=x.device)
+    for e in range(w1.shape[0]):
+        m = expert == e
+        if m.any():
+            y = F.gelu(x[token[m]].float() @ w1[e].float()) @ w2[e].float()
+            out.index_add_(0, token[m], y * weight[m, None].float())
+    return out
+
+
+def checked(fn, ref: torch.Tensor, flush: torch.Tensor) -> float | str:
+    err = (fn().float() - ref).abs().max().item()
+    if err > TOL * (1 + ref.abs().max().item()):
+        return f"wrong ({err:.3g})"
+    return time_ms(fn, flush)
+
+
+def grouped_mm_layer(x, token, expert, weight, w1, w2) -> torch.Tensor:
+    """Grouped GEMM over a flat list: sort by expert, two torch._grouped_mm
+    calls with GELU between, then the weighted sum back per token."""
+    num_experts = w1.shape[0]
+    order = torch.sort(expert, stable=True).indices
+    counts = torch.zeros(num_experts, dtype=torch.int32, device=x.device).scatter_add_(
+        0, expert, torch.ones_like(expert, dtype=torch.int32))
+    offs = torch.cumsum(counts, 0, dtype=torch.int32)
+    tok = token[order]
+    h = F.gelu(torch._grouped_mm(x[tok], w1, offs=offs))
+    y = torch._grouped_mm(h, w2, offs=offs).float() * weight[order, None].float()
+    return torch.zeros(x.shape[0], x.shape[1], device=x.device).index_add_(0, tok, y).to(x.dtype)
+
+
+def loop_layer(x, token, expert, weight, w1, w2) -> torch.Tensor:
+    out = torch.zeros(x.shape[0], x.shape[1], device=x.device)
+    order = torch.sort(expert, stable=True).indices
+    counts = torch.bincount(expert, minlength=w1.shape[0]).tolist()  # host sync
+    start = 0
+    for e, n in enumerate(counts):
+        if n:
+            rows = order[start:start + n]
+            y = F.gelu(x[token[rows]] @ w1[e]) @ w2[e]
+            out.index_add_(0, token[rows], y.float() * weight[rows, None].float())
+        start += n
+    return out.to(x.dtype)
+
+
+def graph_of(fn):
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g.replay
+
+
+def fmt(v) -> str:
+    return f"{v:.3f}" if isinstance(v, float) else str(v)
+
+
+def layer_table(flush: torch.Tensor) -> list[str]:
+    lines = ["| shape | routing | ours (graph) | ours (eager) | torch._grouped_mm | per-expert loop |",
+             "|---|---|---:|---:|---:|---:|"]
+    print("\n".join(lines), flush=True)
+    for shape_name in ("fine_grained", "mixtral"):
+        shape = SHAPES[shape_name]
+        for routing in ("random", "zipf_perm"):
+            x, idx, gates, w1, w2 = make_layer(shape, routing, 0)
+            k = idx.shape[1]
+            token = torch.arange(x.shape[0], device=x.device).repeat_interleave(k)
+            expert, weight = idx.reshape(-1), gates.reshape(-1)
+            ref = reference_fp32(x, token, expert, weight, w1, w2)
+            row = [shape_name, routing]
+            ours = lambda: moe_forward(x, idx, gates, w1, w2)  # noqa: E731
+            t_eager = checked(ours, ref, flush)
+            t_graph = time_ms(graph_of(ours), flush) if isinstance(t_eager, float) else "-"
+            row += [fmt(t_graph), fmt(t_eager)]
+            try:
+                row.append(fmt(checked(lambda: grouped_mm_layer(x, token, expert, weight, w1, w2), ref, flush)))
+            except RuntimeError as e:
+                row.append(f"unavailable ({str(e).splitlines()[0][:60]})")
+            row.append(fmt(checked(lambda: loop_layer(x, token, expert, weight, w1, w2), ref, flush)))
+            lines.append("| " + " | ".join(row) + " |")
+            print(lines[-1], flush=True)
+            del x, idx, gates, w1, w2, ref
+            torch.cuda.empty_cache()
+    return lines
+
+
+def rounding_table(flush: torch.Tensor) -> list[str]:
+    lines = ["| shape | tokens | routing | ours top-k | ours TR | gain | ours TR fused: eager / graph | "
+             "grouped_mm top-k | grouped_mm TR | rounding alone (ours): eager / graph |",
+             "|---|---:|---|---:|---:|---:|---:|---:|---:|---:|"]
+    print("\n".join(lines), flush=True)
+    problems = [("fine_grained", 4096), ("fine_grained", 16384), ("mixtral", 4096)]
+    for shape_name, num_tokens in problems:
+        base = SHAPES[shape_name]
+        shape = type(base)(base.name, num_tokens, base.d_model, base.ffn_dim, base.num_experts)
+        x, _, _, w1, w2 = make_layer(shape, "random", 0)
+        e = shape.num_experts
+        for routing in ("uniform", "zipf"):
+            scores = router_scores(routing, num_tokens, e).cuda()
+            plain = top_k_assignments(scores, 2)
+            rounded = token_rounding(scores, 2, 128)
+            row = [shape_name, str(num_tokens), routing]
+            t = {}
+            for label, a in (("topk", plain), ("tr", rounded)):
+                ref = reference_fp32(x, a.token, a.expert, a.weight, w1, w2)
+                t["ours_" + label] = checked(
+                    lambda a=a: moe_forward_assigned(x, a.token, a.expert, a.weight, w1, w2), ref, flush)
+                try:
+                    t["gmm_" + label] = checked(
+                        lambda a=a: grouped_mm_layer(x, a.token, a.expert, a.weight, w1, w2), ref, flush)
+                except RuntimeError as err:
+                    t["gmm_" + label] = f"unavailable ({str(err).splitlines()[0][:40]})"
+                if label == "tr":
+                    fused = lambda: moe_forward_rounded(x, scores, 2, w1, w2)  # noqa: E731
+                    t["fused"] = checked(fused, ref, flush)
+                    t["fused_graph"] = time_ms(graph_of(fused), flush) if isinstance(t["fused"], float) else "-"
+                del ref
+            rounding = lambda: route_rounded(scores, 2, shape.ffn_dim, 128, 128)  # noqa: E731
+            t["rounding"] = time_ms(rounding, flush)
+            t["rounding_graph"] = time_ms(graph_of(rounding), flush)
+            gain = (f"{t['ours_topk'] / t['ours_tr']:.2f}x"
+                    if isinstance(t["ours_topk"], float) and isinstance(t["ours_tr"], float) else "-")
+            row += [fmt(t["ours_topk"]), fmt(t["ours_tr"]), gain, f"{fmt(t['fused'])} / {fmt(t['fused_graph'])}",
+                    fmt(t["gmm_topk"]), fmt(t["gmm_tr"]), f"{fmt(t['rounding'])} / {fmt(t['rounding_graph'])}"]
+            lines.append("| " + " | ".join(row) + " |")
+            print(lines[-1], flush=True)
+        del x, w1, w2
+        torch.cuda.empty_cache()
+    return lines
+
+
+def main() -> None:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--only", choices=["layer", "rounding"])
+    args = p.parse_args()
+    if not torch.cuda.is_available():
+        raise SystemExit("bench_baselines.py needs a GPU")
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+    print(f"GPU: {torch.cuda.get_device_name()}, torch {torch.__version__}; times in ms, median of 20\n", flush=True)
+    if args.only in (None, "layer"):
+        print("## Whole layer, top-2 (T=4096)\n", flush=True)
+        layer_table(flush)
+        print(flush=True)
+    if args.only in (None, "rounding"):
+        print("## Token rounding (tile 128, top-2)\n", flush=True)
+        rounding_table(flush)
+
+
+if __name__ == "__main__":
+    main()

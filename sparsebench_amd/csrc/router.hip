@@ -60,71 +60,119 @@ __global__ void __launch_bounds__(kTopkThreads)
     router_topk_kernel(const float* __restrict__ scores, int64_t num_tokens, int32_t num_experts, int32_t k,
                        float* __restrict__ shifted, int32_t* __restrict__ chunk_counts,
                        int32_t* __restrict__ top_idx, float* __restrict__ top_weight) {
+  // With E <= 256 the shifted scores go through an LDS tile [E][64 tokens]
+  // so that the expert-major stores are 64-token rows, not scattered words.
+  constexpr bool kTile = PER <= 4;
+  constexpr int kTileStride = kTopkTokensPerGroup + 1;
+  constexpr int kPerWave = kTopkTokensPerGroup / 4;
+  // Tokens whose scores are loaded together (all loads in flight at once).
+  constexpr int kBatch = PER <= 2 ? kPerWave : PER <= 4 ? 8 : 4;
   __shared__ int32_t hist[kMaxExperts];
+  __shared__ float tile[kTile ? 64 * PER * kTileStride : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (chunk_counts != nullptr)
     for (int e = tid; e < num_experts; e += kTopkThreads) hist[e] = 0;
   __syncthreads();
 
-  for (int j = 0; j < kTopkTokensPerGroup / 4; ++j) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kTopkTokensPerGroup + wave * (kTopkTokensPerGroup / 4) + j;
-    if (t >= num_tokens) break;
-    float v[PER];
-    uint32_t picked = 0;
+  const int64_t group_base = static_cast<int64_t>(blockIdx.x) * kTopkTokensPerGroup;
+  for (int j0 = 0; j0 < kPerWave; j0 += kBatch) {
+    float vb[kBatch][PER];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      v[i] = e < num_experts ? scores[t * num_experts + e] : 0.0f;
-    }
-    float total = 0.0f;
-    for (int r = 0; r < k; ++r) {
-      float bv = 0.0f;
-      int bi = 0x7fffffff;
+    for (int b = 0; b < kBatch; ++b) {
+      const int64_t t = group_base + wave * kPerWave + j0 + b;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int e = lane + 64 * i;
-        if (e < num_experts && !((picked >> i) & 1u) && (bi == 0x7fffffff || better(v[i], e, bv, bi))) {
-          bv = v[i];
-          bi = e;
+        vb[b][i] = (t < num_tokens && e < num_experts) ? scores[t * num_experts + e] : 0.0f;
+      }
+    }
+    // The k rounds of all kBatch tokens in lockstep: their shuffle chains
+    // are independent, so they overlap instead of running one after another.
+    uint32_t picked[kBatch];
+    float total[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      picked[b] = 0;
+      total[b] = 0.0f;
+    }
+    for (int r = 0; r < k; ++r) {
+      float bv[kBatch];
+      int bi[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        bv[b] = 0.0f;
+        bi[b] = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int e = lane + 64 * i;
+          if (e < num_experts && !((picked[b] >> i) & 1u) && (bi[b] == 0x7fffffff || better(vb[b][i], e, bv[b], bi[b]))) {
+            bv[b] = vb[b][i];
+            bi[b] = e;
+          }
         }
       }
       for (int d = 32; d >= 1; d >>= 1) {
-        const float ov = __shfl_xor(bv, d, 64);
-        const int oi = __shfl_xor(bi, d, 64);
-        if (oi != 0x7fffffff && (bi == 0x7fffffff || better(ov, oi, bv, bi))) {
-          bv = ov;
-          bi = oi;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const float ov = __shfl_xor(bv[b], d, 64);
+          const int oi = __shfl_xor(bi[b], d, 64);
+          if (oi != 0x7fffffff && (bi[b] == 0x7fffffff || better(ov, oi, bv[b], bi[b]))) {
+            bv[b] = ov;
+            bi[b] = oi;
+          }
         }
       }
-      // bi: the r-th best expert, the same in every lane.
-      if ((bi & 63) == lane) picked |= 1u << (bi >> 6);
-      total += bv;  // in pick order, as a sum over the k picks
-      if (lane == 0) {
-        if (top_idx != nullptr) top_idx[t * k + r] = bi;
-        if (top_weight != nullptr) top_weight[t * k + r] = bv;  // raw score; normalized below
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        // bi[b]: the r-th best expert of token b, the same in every lane.
+        if ((bi[b] & 63) == lane) picked[b] |= 1u << (bi[b] >> 6);
+        total[b] += bv[b];  // in pick order, as a sum over the k picks
+        const int64_t t = group_base + wave * kPerWave + j0 + b;
+        if (lane == 0 && t < num_tokens) {
+          if (top_idx != nullptr) top_idx[t * k + r] = bi[b];
+          if (top_weight != nullptr) top_weight[t * k + r] = bv[b];  // raw score; normalized below
+        }
       }
     }
-    // Weights: the picked scores over their sum (lane 0 reads back what it wrote).
-    if (top_weight != nullptr && lane == 0)
-      for (int r = 0; r < k; ++r) top_weight[t * k + r] = top_weight[t * k + r] / total;
-    if (shifted != nullptr) {
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int e = lane + 64 * i;
-        if (e < num_experts) shifted[static_cast<int64_t>(e) * num_tokens + t] = ((picked >> i) & 1u) ? v[i] : v[i] - 1.0f;
+    for (int b = 0; b < kBatch; ++b) {
+      const int t_local = wave * kPerWave + j0 + b;
+      const int64_t t = group_base + t_local;
+      if (t >= num_tokens) break;
+      // Weights: the picked scores over their sum (lane 0 reads back what it wrote).
+      if (top_weight != nullptr && lane == 0)
+        for (int r = 0; r < k; ++r) top_weight[t * k + r] = top_weight[t * k + r] / total[b];
+      if (shifted != nullptr) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int e = lane + 64 * i;
+          if (e < num_experts) {
+            const float sv = ((picked[b] >> i) & 1u) ? vb[b][i] : vb[b][i] - 1.0f;
+            if constexpr (kTile) tile[e * kTileStride + t_local] = sv;
+            else shifted[static_cast<int64_t>(e) * num_tokens + t] = sv;
+          }
+        }
       }
-    }
-    if (chunk_counts != nullptr) {
+      if (chunk_counts != nullptr) {
 #pragma unroll
-      for (int i = 0; i < PER; ++i)
-        if ((picked >> i) & 1u) atomicAdd(&hist[lane + 64 * i], 1);
+        for (int i = 0; i < PER; ++i)
+          if ((picked[b] >> i) & 1u) atomicAdd(&hist[lane + 64 * i], 1);
+      }
     }
   }
-  if (chunk_counts != nullptr) {
-    __syncthreads();
+  __syncthreads();
+  if constexpr (kTile) {
+    if (shifted != nullptr) {
+      for (int i = tid; i < num_experts * kTopkTokensPerGroup; i += kTopkThreads) {
+        const int e = i / kTopkTokensPerGroup, tl = i % kTopkTokensPerGroup;
+        const int64_t t = group_base + tl;
+        if (t < num_tokens) shifted[static_cast<int64_t>(e) * num_tokens + t] = tile[e * kTileStride + tl];
+      }
+    }
+  }
+  if (chunk_counts != nullptr)
     for (int e = tid; e < num_experts; e += kTopkThreads)
       chunk_counts[static_cast<int64_t>(blockIdx.x) * num_experts + e] = hist[e];
-  }
 }
 
 // Inclusive scan over the lanes of one 1024-lane workgroup.
@@ -150,12 +198,29 @@ __global__ void __launch_bounds__(1024)
     router_targets_kernel(const int32_t* __restrict__ chunk_counts, int32_t num_chunks, int32_t num_experts,
                           int64_t num_tokens, int32_t tile, int32_t block_size, int32_t* __restrict__ target,
                           int32_t* __restrict__ padded_offsets, int32_t* __restrict__ error) {
+  __shared__ int32_t counts[kMaxExperts];
   __shared__ int32_t wave_sums[16];
   const int tid = threadIdx.x;
+  for (int e = tid; e < num_experts; e += 1024) counts[e] = 0;
+  __syncthreads();
+  // Column sums of chunk_counts [chunks, E], read in order, 8 loads in flight per lane.
+  constexpr int kPer = 8;
+  const int64_t total_items = static_cast<int64_t>(num_chunks) * num_experts;
+  for (int64_t base = 0; base < total_items; base += 1024 * kPer) {
+    int32_t v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int64_t i = base + u * 1024 + tid;
+      v[u] = i < total_items ? chunk_counts[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      if (v[u] != 0) atomicAdd(&counts[(base + u * 1024 + tid) % num_experts], v[u]);
+  }
+  __syncthreads();
   int32_t padded = 0;
   if (tid < num_experts) {
-    int32_t f = 0;
-    for (int b = 0; b < num_chunks; ++b) f += chunk_counts[static_cast<int64_t>(b) * num_experts + tid];
+    const int32_t f = counts[tid];
     const int32_t low = f / tile * tile;
     const int32_t high = low + (f % tile > 0 ? tile : 0);
     int32_t rounded = (high - f < f - low) ? high : low;  // nearest, ties down
@@ -173,11 +238,34 @@ __global__ void __launch_bounds__(1024)
   }
 }
 
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int lane = threadIdx.x & 63;
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// hist[bin] += 1 for every active lane, one LDS atomic per distinct bin in
+// the wave (lanes with the same bin found by one ballot per bin bit).
+// Softmax scores share few top-byte values, so plain per-lane atomics
+// would pile onto one or two addresses.
+__device__ __forceinline__ void wave_hist_add(int32_t* hist, uint32_t bin, bool active) {
+  uint64_t peers = __ballot(active);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const bool bit = (bin >> b) & 1u;
+    const uint64_t ones = __ballot(active && bit);
+    peers &= bit ? ones : ~ones;
+  }
+  if (active && (peers & lanes_below()) == 0) atomicAdd(&hist[bin], __popcll(peers));
+}
+
+constexpr int kSelectLdsTokens = 32768;  // a column of up to this many keys stays in LDS (128 KB)
+
 // One workgroup per expert e: which tokens it keeps, and their rows.
 __global__ void __launch_bounds__(kSelectThreads)
     router_select_kernel(const float* __restrict__ shifted, int64_t num_tokens, const int32_t* __restrict__ target,
                          const int32_t* __restrict__ padded_offsets, uint32_t* __restrict__ keep_mask,
                          int32_t* __restrict__ keep_prefix, int32_t* __restrict__ row_token) {
+  __shared__ uint32_t keys[kSelectLdsTokens];
   __shared__ int32_t hist[256];
   __shared__ int32_t wave_sums[16];
   __shared__ uint32_t s_prefix, s_prefix_mask;
@@ -190,6 +278,27 @@ __global__ void __launch_bounds__(kSelectThreads)
   const int64_t words = (num_tokens + 31) / 32;
   uint32_t* mask = keep_mask + static_cast<int64_t>(e) * words;
   int32_t* pref = keep_prefix + static_cast<int64_t>(e) * words;
+
+  // Keys of the column, computed once (in LDS when they fit).
+  const bool in_lds = num_tokens <= kSelectLdsTokens;
+  if (in_lds) {
+    constexpr int kPer = 8;
+    for (int64_t base = 0; base < num_tokens; base += kSelectThreads * kPer) {
+      float v[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int64_t t = base + u * kSelectThreads + tid;
+        v[u] = t < num_tokens ? col[t] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int64_t t = base + u * kSelectThreads + tid;
+        if (t < num_tokens) keys[t] = sort_key(v[u]);
+      }
+    }
+    __syncthreads();
+  }
+  auto key_at = [&](int64_t t) -> uint32_t { return in_lds ? keys[t] : sort_key(col[t]); };
 
   // Threshold key and the last tie kept: keep t iff key > thr, or
   // key == thr and t <= cut.
@@ -210,21 +319,41 @@ __global__ void __launch_bounds__(kSelectThreads)
       for (int b = tid; b < 256; b += kSelectThreads) hist[b] = 0;
       __syncthreads();
       const uint32_t pre = s_prefix, pmask = s_prefix_mask;
-      for (int64_t t = tid; t < num_tokens; t += kSelectThreads) {
-        const uint32_t key = sort_key(col[t]);
-        if ((key & pmask) == pre) atomicAdd(&hist[(key >> shift) & 255u], 1);
+      for (int64_t base = 0; base < num_tokens; base += kSelectThreads) {  // same trip count in every lane
+        const int64_t t = base + tid;
+        const uint32_t key = t < num_tokens ? key_at(t) : 0u;
+        wave_hist_add(hist, (key >> shift) & 255u, t < num_tokens && (key & pmask) == pre);
       }
       __syncthreads();
-      if (tid == 0) {
-        int32_t rem = s_remaining, cum = 0;
-        for (int b = 255; b >= 0; --b) {
-          if (cum + hist[b] >= rem) {
-            s_prefix = pre | (static_cast<uint32_t>(b) << shift);
-            s_prefix_mask = pmask | (255u << shift);
-            s_remaining = rem - cum;
-            break;
+      if (tid < 64) {
+        // Wave 0: lane l holds bins 255-4l .. 252-4l (descending). A suffix
+        // count from the top finds the bin where the rem-th largest falls.
+        const int32_t rem = s_remaining;
+        int32_t c[4], own = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          c[q] = hist[255 - 4 * tid - q];
+          own += c[q];
+        }
+        int32_t incl = own;  // keys in bins above and including this lane's four
+        for (int d = 1; d < 64; d <<= 1) {
+          const int32_t below = __shfl_up(incl, d, 64);
+          if (tid >= d) incl += below;
+        }
+        int32_t above = incl - own;  // keys in higher bins than this lane's
+        // The lane whose four bins reach rem: the first with incl >= rem.
+        const uint64_t reach = __ballot(incl >= rem);
+        if (reach != 0 && tid == __builtin_ctzll(reach)) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (above + c[q] >= rem) {
+              s_prefix = pre | (static_cast<uint32_t>(255 - 4 * tid - q) << shift);
+              s_prefix_mask = pmask | (255u << shift);
+              s_remaining = rem - above;
+              break;
+            }
+            above += c[q];
           }
-          cum += hist[b];
         }
       }
       __syncthreads();
@@ -236,7 +365,7 @@ __global__ void __launch_bounds__(kSelectThreads)
     int32_t carry = 0;
     for (int64_t base = 0; base < num_tokens; base += kSelectThreads) {
       const int64_t t = base + tid;
-      const int32_t is_tie = (t < num_tokens && sort_key(col[t]) == thr) ? 1 : 0;
+      const int32_t is_tie = (t < num_tokens && key_at(t) == thr) ? 1 : 0;
       int32_t chunk_total;
       const int32_t incl = block_scan_1024(is_tie, wave_sums, &chunk_total);
       if (is_tie && carry + incl == ties) s_cut = t;
@@ -258,7 +387,7 @@ __global__ void __launch_bounds__(kSelectThreads)
         if (t >= num_tokens) break;
         bool keep = keep_all;
         if (!keep_all) {
-          const uint32_t key = sort_key(col[t]);
+          const uint32_t key = key_at(t);
           keep = key > thr || (key == thr && t <= cut);
         }
         if (keep) bits |= 1u << b;
@@ -321,17 +450,31 @@ __global__ void __launch_bounds__(64 * kTokenWaves)
 }
 
 // token_offsets = exclusive scan of kept_count; token_offsets[T] = N.
+// Each lane takes 16 consecutive tokens, so one workgroup scan covers 16K
+// tokens (one pass at the benchmark sizes).
 __global__ void __launch_bounds__(1024)
     router_scan_kernel(const int32_t* __restrict__ kept_count, int64_t num_tokens, int32_t* __restrict__ token_offsets,
                        int32_t* __restrict__ num_assignments) {
   __shared__ int32_t wave_sums[16];
+  constexpr int kPer = 16;
   int32_t carry = 0;
-  for (int64_t base = 0; base < num_tokens; base += 1024) {
-    const int64_t t = base + threadIdx.x;
-    const int32_t v = t < num_tokens ? kept_count[t] : 0;
+  for (int64_t base = 0; base < num_tokens; base += 1024 * kPer) {
+    const int64_t t0 = base + static_cast<int64_t>(threadIdx.x) * kPer;
+    int32_t v[kPer];
+    int32_t own = 0;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      v[u] = t0 + u < num_tokens ? kept_count[t0 + u] : 0;
+      own += v[u];
+    }
     int32_t chunk_total;
-    const int32_t incl = block_scan_1024(v, wave_sums, &chunk_total);
-    if (t < num_tokens) token_offsets[t] = carry + incl - v;
+    const int32_t incl = block_scan_1024(own, wave_sums, &chunk_total);
+    int32_t run = carry + incl - own;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      if (t0 + u < num_tokens) token_offsets[t0 + u] = run;
+      run += v[u];
+    }
     carry += chunk_total;
   }
   if (threadIdx.x == 0) {

@@ -151,7 +151,7 @@ __global__ void __launch_bounds__(Cfg::kThreads)
                    int32_t num_slices, int32_t zero_dead_rows, int32_t group) {
   using ML = DmaMainloop<Cfg>;
   constexpr int BM = Cfg::BM, BN = Cfg::BN;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsAlloc];
 
   const int live_rb = zero_dead_rows ? num_row_blocks : live_row_blocks(row_offsets, num_row_blocks);
   const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
@@ -191,18 +191,12 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   typename ML::Acc acc;
   ML::run(lds, src, (end - begin) * DsdDmaSrc<Cfg>::kStepsPerBlock, acc);
 
-#pragma unroll
-  for (int jn = 0; jn < Cfg::TN; ++jn)
-#pragma unroll
-    for (int i = 0; i < Cfg::TM; ++i) {
-      uint16_t* row = out_tile + static_cast<int64_t>(ML::out_row(i)) * d_model;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x16_t& a = acc[jn][i];
-        *reinterpret_cast<u32x2_t*>(row + ML::out_col(jn, g)) =
-            u32x2_t{pack_bf16x2(a[4 * g], a[4 * g + 1]), pack_bf16x2(a[4 * g + 2], a[4 * g + 3])};
-      }
-    }
+  // bf16, staged in LDS, then whole row segments per store instruction.
+  // Plain stores: the combine reads these rows right away, partly from L2.
+  ML::stage_tile(lds, acc, [](float v) { return v; });
+  ML::for_each_staged_chunk(lds, [&](int r, int col, u32x4_t v) {
+    *reinterpret_cast<u32x4_t*>(out_tile + static_cast<int64_t>(r) * d_model + col) = v;
+  });
 }
 
 // Persistent form (DmaMainloop::run_tiles): about one workgroup per CU slot,
@@ -323,7 +317,7 @@ __global__ void __launch_bounds__(Cfg::kThreads)
                           const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ col_indices,
                           uint16_t* __restrict__ out, int64_t nnz, int64_t w_rows, int32_t num_row_blocks,
                           int32_t d_model, int32_t num_slices, int32_t zero_dead_rows, int32_t group) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsAlloc];
   DsdTiles<Cfg> sched;
   sched.blocks = blocks;
   sched.w = w;
@@ -439,6 +433,13 @@ int dispatch_dsd(int variant, Args... args) {
     case 36:
       if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 4, 0, 2>>(args...);
       else return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 2, 0, 2>>(args...);
+    case 37:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 32, 6, 2, 4, 0, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 32, 6, 2, 2, 0, 2>>(args...);
+    case 38:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 32, 5, 2, 4, 0, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 32, 5, 2, 2, 0, 2>>(args...);
+    case 39: return launch_dsd_dma<DmaCfg<BM, 128, 32, 8, 2, 2, 0, 2>>(args...);
     case 41:
       if constexpr (BM == 128) return launch_dsd_persistent<DmaCfg<BM, 256, 64, 3, 2, 4, 0, 2>>(args...);
       else return launch_dsd_persistent<DmaCfg<BM, 256, 64, 3, 2, 2, 0, 2>>(args...);
@@ -481,17 +482,15 @@ extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offs
   // Default, from timing every variant on the benchmark shapes (MI355X):
   // 128 x 512 tiles, 4 waves, BK 32 x 4-stage LDS-DMA ring with non-temporal
   // W loads. The row's reduction depth (K = F per expert, read from the
-  // buffer shape: nnz / num_row_blocks blocks per row) moves the choice:
-  // with K >= 8192 there are enough K steps per tile that 128 x 128 tiles
-  // balance the CUs better; with K < 2048 a tile is so short that its
-  // prologue and epilogue matter, and the persistent 128 x 256 form, which
-  // overlaps them with the next tile's loads, wins.
+  // buffer shape: nnz / num_row_blocks blocks per row) moves the choice: at
+  // both ends (K >= 8192: few row blocks, so few wide tiles per CU; K < 2048:
+  // short tiles) 128 x 256 tiles with 8 waves and a 3-stage BK 64 ring win.
   const int64_t row_k = num_row_blocks > 0 ? nnz / num_row_blocks * block_size : 0;
-  int variant = forced > 0 ? forced : (row_k >= 8192 ? 11 : row_k < 2048 ? 41 : 32);
+  int variant = forced > 0 ? forced : (row_k >= 8192 || row_k < 2048 ? 25 : 32);
   if (d_model % 256 != 0 && (variant == 2 || variant == 4 || variant == 5 || variant == 6 || variant == 14 ||
                              variant == 15 || variant == 16 || variant == 17 || variant == 24 || variant == 25 ||
-                             variant == 26 || variant == 34 || variant == 35 || variant == 36 || variant == 41 ||
-                             variant == 44))
+                             variant == 26 || variant == 34 || variant == 35 || variant == 36 || variant == 37 ||
+                             variant == 38 || variant == 41 || variant == 44))
     variant = 1;
   if (d_model % 512 != 0 && ((variant >= 31 && variant <= 33) || variant == 42)) variant = d_model % 256 == 0 ? 25 : 21;
   if (block_size == 128)

@@ -162,7 +162,7 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   using ML = DmaMainloop<Cfg>;
   constexpr int BN = Cfg::BN;
   static_assert(Cfg::BM == kBS, "one row block per tile");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsAlloc];
 
   const int live_rb = live_row_blocks(row_offsets, num_row_blocks);
   const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
@@ -199,26 +199,17 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   typename ML::Acc acc;
   ML::run(lds, src, d_model / Cfg::BK, acc);
 
-  // C[m, f] -> block begin + f/128, row m, column f % 128; 4 columns per store.
+  // GELU, bf16, staged in LDS; then C[m, f] -> block begin + f/128, row m,
+  // column f % 128, whole 256-byte block rows per store instruction.
+  if (apply_gelu)
+    ML::stage_tile(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
+  else
+    ML::stage_tile(lds, acc, [](float v) { return v; });
   uint16_t* blocks = out + static_cast<int64_t>(begin) * kBS * kBS;
-#pragma unroll
-  for (int jn = 0; jn < Cfg::TN; ++jn)
-#pragma unroll
-    for (int i = 0; i < Cfg::TM; ++i) {
-      const int m = ML::out_row(i);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int f = n0 + ML::out_col(jn, g);
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[jn][i][4 * g + e];
-          if (apply_gelu) v[e] = kFastGelu ? gelu_erf_fast(v[e]) : gelu_erf_libm(v[e]);
-        }
-        *reinterpret_cast<u32x2_t*>(blocks + static_cast<int64_t>(f / kBS) * kBS * kBS + m * kBS + (f % kBS)) =
-            u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-      }
-    }
+  ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
+    const int f = n0 + col;
+    ML::store_streaming(blocks + static_cast<int64_t>(f / kBS) * kBS * kBS + m * kBS + (f % kBS), v);
+  });
 }
 
 // Persistent form (DmaMainloop::run_tiles): gridDim.x workgroups, about one
@@ -375,7 +366,7 @@ __global__ void __launch_bounds__(Cfg::kThreads)
                           int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t num_row_blocks,
                           int32_t num_slices, int32_t apply_gelu, int32_t group) {
   static_assert(Cfg::BM == kBS, "one row block per tile");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsAlloc];
   SddTiles<Cfg, kFastGelu> sched;
   sched.x = x;
   sched.w1 = w1;
@@ -483,6 +474,9 @@ int dispatch_sdd(int variant, Args... args) {
     case 34: return launch_sdd_dma<DmaCfg<128, 256, 32, 3, 2, 4, 0, 2>, kFastGelu>(args...);
     case 35: return launch_sdd_dma<DmaCfg<128, 256, 32, 3, 2, 2, 0, 2>, kFastGelu>(args...);
     case 36: return launch_sdd_dma<DmaCfg<128, 256, 64, 2, 2, 4, 0, 2>, kFastGelu>(args...);
+    case 37: return launch_sdd_dma<DmaCfg<128, 256, 32, 6, 2, 4, 0, 2>, kFastGelu>(args...);
+    case 38: return launch_sdd_dma<DmaCfg<128, 256, 32, 5, 2, 4, 0, 2>, kFastGelu>(args...);
+    case 39: return launch_sdd_dma<DmaCfg<128, 128, 32, 8, 2, 2, 0, 2>, kFastGelu>(args...);
     case 41: return launch_sdd_persistent<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2>, kFastGelu>(args...);
     case 43: return launch_sdd_persistent<DmaCfg<128, 128, 64, 2, 2, 2, 0, 2>, kFastGelu>(args...);
     case 44: return launch_sdd_persistent<DmaCfg<128, 256, 32, 3, 2, 4, 0, 2>, kFastGelu>(args...);
@@ -522,9 +516,9 @@ extern "C" int sb_sdd(const void* x, const void* w1, const int32_t* row_token, c
   const int gelu_mode = tuning_override("SPARSEBENCH_GELU_LIBM");
   // Default, from timing every variant on the benchmark shapes (MI355X):
   // 128 x 256 tiles, 8 waves, 3-stage LDS-DMA ring with non-temporal weight
-  // loads; with a deep reduction (D >= 4096) 128 x 512 tiles, 4 waves,
+  // loads; with a deeper reduction (D >= 2048) 128 x 512 tiles, 4 waves,
   // BK 32 x 4 stages, which halve the x re-reads per FLOP.
-  int variant = forced > 0 ? forced : (d_model >= 4096 ? 32 : 25);
+  int variant = forced > 0 ? forced : (d_model >= 2048 ? 32 : 25);
   if (ffn_dim % 512 != 0 && variant >= 31 && variant <= 33) variant = 25;
   if (gelu_mode > 0)
     return dispatch_sdd<false>(variant, x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model,

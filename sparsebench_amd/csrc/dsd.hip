@@ -433,6 +433,30 @@ int dispatch_dsd(int variant, Args... args) {
     case 36:
       if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 4, 0, 2>>(args...);
       else return launch_dsd_dma<DmaCfg<BM, 256, 64, 2, 2, 2, 0, 2>>(args...);
+    case 51:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 4, 0, 2, 1>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 2, 0, 2, 1>>(args...);
+    case 52: return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 1>>(args...);
+    case 53:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 32, 5, 2, 4, 0, 2, 1>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 32, 5, 2, 2, 0, 2, 1>>(args...);
+    case 54:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 4, 0, 2, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 2, 0, 2, 2>>(args...);
+    case 55: return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 2>>(args...);
+    // 8 waves of 64 x 128 (a 64-row block takes the 4-wave form).
+    case 56:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 2, 4, 0, 2, 0>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 0>>(args...);
+    case 57:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 2, 4, 0, 2, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 2>>(args...);
+    case 58:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 2, 4, 0, 2, 1>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 1>>(args...);
+    case 59:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 64, 2, 2, 4, 0, 2, 2>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 512, 64, 2, 1, 4, 0, 2, 2>>(args...);
     case 37:
       if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 32, 6, 2, 4, 0, 2>>(args...);
       else return launch_dsd_dma<DmaCfg<BM, 256, 32, 6, 2, 2, 0, 2>>(args...);
@@ -479,20 +503,24 @@ extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offs
     return fail(SB_ERR_INVALID, "blocks and w must be 16-byte aligned");
   const hipStream_t s = as_stream(stream);
   const int forced = tuning_override("SPARSEBENCH_DSD_VARIANT");
-  // Default, from timing every variant on the benchmark shapes (MI355X):
-  // 128 x 512 tiles, 4 waves, BK 32 x 4-stage LDS-DMA ring with non-temporal
-  // W loads. The row's reduction depth (K = F per expert, read from the
-  // buffer shape: nnz / num_row_blocks blocks per row) moves the choice: at
-  // both ends (K >= 8192: few row blocks, so few wide tiles per CU; K < 2048:
-  // short tiles) 128 x 256 tiles with 8 waves and a 3-stage BK 64 ring win.
+  // Default, from timing every variant on the benchmark shapes (MI355X,
+  // samples interleaved across variants): 128 x 512 tiles, 4 waves of
+  // 128 x 128, BK 32 x 4-stage LDS-DMA ring with non-temporal W loads. The
+  // row's reduction depth (K = F per expert, read from the buffer shape:
+  // nnz / num_row_blocks blocks per row) moves the choice: with K >= 8192
+  // (few row blocks, so few wide tiles per CU) 128 x 256 tiles of 8 waves;
+  // with K < 2048 (short tiles) 128 x 512 tiles of 8 waves of 64 x 128.
   const int64_t row_k = num_row_blocks > 0 ? nnz / num_row_blocks * block_size : 0;
-  int variant = forced > 0 ? forced : (row_k >= 8192 || row_k < 2048 ? 25 : 32);
+  int variant = forced > 0 ? forced : (row_k >= 8192 ? 25 : row_k < 2048 ? 58 : 32);
   if (d_model % 256 != 0 && (variant == 2 || variant == 4 || variant == 5 || variant == 6 || variant == 14 ||
                              variant == 15 || variant == 16 || variant == 17 || variant == 24 || variant == 25 ||
                              variant == 26 || variant == 34 || variant == 35 || variant == 36 || variant == 37 ||
-                             variant == 38 || variant == 41 || variant == 44))
+                             variant == 38 || variant == 41 || variant == 44 || variant == 51 || variant == 53 ||
+                             variant == 54))
     variant = 1;
-  if (d_model % 512 != 0 && ((variant >= 31 && variant <= 33) || variant == 42)) variant = d_model % 256 == 0 ? 25 : 21;
+  if (d_model % 512 != 0 &&
+      ((variant >= 31 && variant <= 33) || variant == 42 || variant == 52 || (variant >= 55 && variant <= 59)))
+    variant = d_model % 256 == 0 ? 25 : 21;
   if (block_size == 128)
     return dispatch_dsd<128>(variant, blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
                              zero_dead_rows, s);

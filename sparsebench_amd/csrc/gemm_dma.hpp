@@ -61,10 +61,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 // CPA / CPB: cache policy of the A / B loads (buffer instruction bits; 2 = nt,
 // a streaming hint that keeps the read-once weight stream from displacing
 // reusable lines).
-template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0>
+// PIPE: fragment schedule inside a K step. 0: per 16-deep sub-step, read
+// its fragments then run its MFMAs (the compiler schedules). 1: two
+// fragment register sets, sub-step s+1's LDS reads issued among sub-step
+// s's MFMAs (scheduling groups pin the interleave). 2: the two register
+// sets without the pinned interleave.
+template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0, int PIPE_ = 0>
 struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_;
   static constexpr int CPA = CPA_, CPB = CPB_;
+  static constexpr int PIPE = PIPE_;
   static constexpr int WM = WM_, WN = WN_;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
@@ -136,6 +142,19 @@ struct BDmaPos {
     }
   }
 };
+
+// Scheduling groups for one sub-step: MFMA, then up to kPer DS reads,
+// kMfma times (mask 0x008 = MFMA, 0x100 = DS read).
+template <int Q, int kMfma, int kReads, int kPer>
+__device__ __forceinline__ void sched_interleave() {
+  if constexpr (Q < kMfma) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int left = kReads - Q * kPer;
+    constexpr int n = left <= 0 ? 0 : (left < kPer ? left : kPer);
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+    sched_interleave<Q + 1, kMfma, kReads, kPer>();
+  }
+}
 
 // s_waitcnt vmcnt(later * L) for a run-time `later` in [0, MAXL].
 template <int L, int MAXL>
@@ -210,13 +229,13 @@ struct DmaMainloop {
       const int chunk = 4 * (blk ^ (jj >> 2)) + 2 * (g & 1) + ((jj & 3) >> 1);
       b_off[jn] = krow * Cfg::kBRowBytes + chunk * 16 + (jj & 1) * 8;
     }
-#pragma unroll
-    for (int s = 0; s < Cfg::BK / 16; ++s) {
-      bf16x8_t a[Cfg::TM];
+    constexpr int kSub = Cfg::BK / 16;
+    auto read_a = [&](int s, bf16x8_t (&a)[Cfg::TM]) {
 #pragma unroll
       for (int i = 0; i < Cfg::TM; ++i)
         a[i] = *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * s + h) ^ a_swz[i]) << 4));
-      bf16x8_t b[Cfg::TN];
+    };
+    auto read_b = [&](int s, bf16x8_t (&b)[Cfg::TN]) {
 #pragma unroll
       for (int jn = 0; jn < Cfg::TN; ++jn) {
         const uint8_t* p = bs + b_off[jn] + 16 * s * Cfg::kBRowBytes;
@@ -224,11 +243,47 @@ struct DmaMainloop {
         const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * Cfg::kBRowBytes));
         b[jn] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
+    };
+    auto mfmas = [&](const bf16x8_t (&a)[Cfg::TM], const bf16x8_t (&b)[Cfg::TN]) {
 #pragma unroll
       for (int jn = 0; jn < Cfg::TN; ++jn)
 #pragma unroll
         for (int i = 0; i < Cfg::TM; ++i)
           acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[jn], a[i], acc[jn][i], 0, 0, 0);
+    };
+    if constexpr (Cfg::PIPE == 0) {
+#pragma unroll
+      for (int s = 0; s < kSub; ++s) {
+        bf16x8_t a[Cfg::TM], b[Cfg::TN];
+        read_a(s, a);
+        read_b(s, b);
+        mfmas(a, b);
+      }
+    } else {
+      bf16x8_t a[2][Cfg::TM], b[2][Cfg::TN];
+      read_a(0, a[0]);
+      read_b(0, b[0]);
+#pragma unroll
+      for (int s = 0; s < kSub; ++s) {
+        if (s + 1 < kSub) {
+          read_a(s + 1, a[(s + 1) & 1]);
+          read_b(s + 1, b[(s + 1) & 1]);
+        }
+        mfmas(a[s & 1], b[s & 1]);
+      }
+      if constexpr (Cfg::PIPE == 1) {
+        // Interleave: the first sub-step's reads, then per later sub-step
+        // its MFMAs alternating with the next sub-step's reads.
+        constexpr int kMfma = Cfg::TM * Cfg::TN;
+        constexpr int kReads = Cfg::TM + 2 * Cfg::TN;
+        constexpr int kPer = (kReads + kMfma - 1) / kMfma;
+        __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS reads of sub-step 0
+#pragma unroll
+        for (int s = 0; s < kSub; ++s) {
+          if (s + 1 < kSub) sched_interleave<0, kMfma, kReads, kPer>();
+          else __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
+        }
+      }
     }
   }
 

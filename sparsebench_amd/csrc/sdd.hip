@@ -477,6 +477,15 @@ int dispatch_sdd(int variant, Args... args) {
     case 37: return launch_sdd_dma<DmaCfg<128, 256, 32, 6, 2, 4, 0, 2>, kFastGelu>(args...);
     case 38: return launch_sdd_dma<DmaCfg<128, 256, 32, 5, 2, 4, 0, 2>, kFastGelu>(args...);
     case 39: return launch_sdd_dma<DmaCfg<128, 128, 32, 8, 2, 2, 0, 2>, kFastGelu>(args...);
+    case 51: return launch_sdd_dma<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 1>, kFastGelu>(args...);
+    case 52: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 1, 4, 0, 2, 1>, kFastGelu>(args...);
+    case 53: return launch_sdd_dma<DmaCfg<128, 256, 32, 5, 2, 4, 0, 2, 1>, kFastGelu>(args...);
+    case 54: return launch_sdd_dma<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 2>, kFastGelu>(args...);
+    case 55: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 1, 4, 0, 2, 2>, kFastGelu>(args...);
+    case 56: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 0>, kFastGelu>(args...);
+    case 57: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 2>, kFastGelu>(args...);
+    case 58: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 1>, kFastGelu>(args...);
+    case 59: return launch_sdd_dma<DmaCfg<128, 512, 64, 2, 2, 4, 0, 2, 2>, kFastGelu>(args...);
     case 41: return launch_sdd_persistent<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2>, kFastGelu>(args...);
     case 43: return launch_sdd_persistent<DmaCfg<128, 128, 64, 2, 2, 2, 0, 2>, kFastGelu>(args...);
     case 44: return launch_sdd_persistent<DmaCfg<128, 256, 32, 3, 2, 4, 0, 2>, kFastGelu>(args...);
@@ -514,12 +523,16 @@ extern "C" int sb_sdd(const void* x, const void* w1, const int32_t* row_token, c
   const hipStream_t s = as_stream(stream);
   const int forced = tuning_override("SPARSEBENCH_SDD_VARIANT");
   const int gelu_mode = tuning_override("SPARSEBENCH_GELU_LIBM");
-  // Default, from timing every variant on the benchmark shapes (MI355X):
-  // 128 x 256 tiles, 8 waves, 3-stage LDS-DMA ring with non-temporal weight
-  // loads; with a deeper reduction (D >= 2048) 128 x 512 tiles, 4 waves,
-  // BK 32 x 4 stages, which halve the x re-reads per FLOP.
-  int variant = forced > 0 ? forced : (d_model >= 2048 ? 32 : 25);
-  if (ffn_dim % 512 != 0 && variant >= 31 && variant <= 33) variant = 25;
+  // Default, from timing every variant on the benchmark shapes (MI355X,
+  // samples interleaved across variants): 128 x 512 tiles of 8 waves, each
+  // 64 x 128 (8 MFMAs per 16-deep sub-step: enough work to cover the LDS
+  // fragment reads, 2 waves per SIMD), non-temporal weight loads; a 2-stage
+  // BK 64 ring, or with a deep reduction (D >= 4096) a 4-stage BK 32 ring
+  // with the fragment reads of the next sub-step interleaved. F must be a
+  // multiple of 512; otherwise 128 x 256 tiles of 8 waves.
+  int variant = forced > 0 ? forced : (d_model >= 4096 ? 58 : 59);
+  if (ffn_dim % 512 != 0 && ((variant >= 31 && variant <= 33) || variant == 52 || (variant >= 55 && variant <= 59)))
+    variant = 25;
   if (gelu_mode > 0)
     return dispatch_sdd<false>(variant, x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model,
                                ffn_dim, num_experts, num_row_blocks, apply_gelu, s);

@@ -9,6 +9,8 @@ Layer pipelines (everything from the routing to the [T, D] output is timed,
 host syncs included):
   ours          moe_forward: GPU routing -> SDD (+ gather, GELU) -> DSD -> combine;
                 no host sync. Timed eagerly, and as a captured graph.
+  ours fused    moe_forward(fused_combine=True): the combine inside the DSD
+                kernel (same bits; graph).
   grouped_mm    sort copies by expert -> torch._grouped_mm -> GELU ->
                 torch._grouped_mm -> unsort -> weighted sum (torch ops, no sync).
   loop          per expert: x[tokens] @ w1[e] -> GELU -> @ w2[e], expert counts
@@ -118,8 +120,9 @@ def fmt(v) -> str:
 
 
 def layer_table(flush: torch.Tensor) -> list[str]:
-    lines = ["| shape | routing | ours (graph) | ours (eager) | torch._grouped_mm | per-expert loop |",
-             "|---|---|---:|---:|---:|---:|"]
+    lines = ["| shape | routing | ours (graph) | ours (eager) | ours fused combine (graph) | torch._grouped_mm | "
+             "per-expert loop |",
+             "|---|---|---:|---:|---:|---:|---:|"]
     print("\n".join(lines), flush=True)
     for shape_name in ("fine_grained", "mixtral"):
         shape = SHAPES[shape_name]
@@ -134,6 +137,9 @@ def layer_table(flush: torch.Tensor) -> list[str]:
             t_eager = checked(ours, ref, flush)
             t_graph = time_ms(graph_of(ours), flush) if isinstance(t_eager, float) else "-"
             row += [fmt(t_graph), fmt(t_eager)]
+            fused = lambda: moe_forward(x, idx, gates, w1, w2, fused_combine=True)  # noqa: E731
+            t_fused = checked(fused, ref, flush)
+            row.append(fmt(time_ms(graph_of(fused), flush)) if isinstance(t_fused, float) else fmt(t_fused))
             try:
                 row.append(fmt(checked(lambda: grouped_mm_layer(x, token, expert, weight, w1, w2), ref, flush)))
             except RuntimeError as e:

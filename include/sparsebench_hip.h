@@ -94,6 +94,22 @@ int sb_combine(const void* y, const int32_t* copy_row, const void* gates, int32_
                int64_t num_tokens, int32_t k, int64_t d_model, int64_t y_rows, const int32_t* valid_tokens,
                void* stream);
 
+/* Replaces the last two steps of moe_forward, dsd_cuda version 5 then the
+ * combine (sparsebench/moe.py:48-54, csrc/dsd_v5.cu:106-123), with one
+ * kernel. y [num_row_blocks*128, D] bf16 receives the DSD rows as sb_dsd
+ * (zero_dead_rows = 0) writes them; out [T, D] bf16 receives exactly what
+ * sb_combine(y, copy_row, gates, ...) would write, bit for bit: the tile
+ * that writes a token's last routed row (per 256/512-column slice) sums the
+ * token's rows in slot order. Tokens with no routed copy get a zero row.
+ * Block size 128, D % 256 == 0; row_token / copy_row as sb_routing writes
+ * them; gates [T, k] of gate_dtype; valid_tokens as for sb_combine.
+ * counters: T * (D / 256) int32, all zero on entry and left zero on return;
+ * two calls in flight at once must not share one counters buffer. */
+int sb_dsd_combine(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices,
+                   const int32_t* row_token, const int32_t* copy_row, const void* gates, int32_t gate_dtype, void* y,
+                   void* out, int32_t* counters, int64_t nnz, int64_t w_rows, int64_t num_row_blocks,
+                   int64_t d_model, int64_t num_tokens, int32_t k, const int32_t* valid_tokens, void* stream);
+
 /* ---- Routing given as assignments (sparsebench/moe.py:59-91) ---------- */
 
 /* Replaces the routing of moe_forward_assigned (sparsebench/moe.py:77-82:

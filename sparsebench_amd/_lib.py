@@ -50,6 +50,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.POINTER(_i64)],
     ),
     "sb_router_topk": (_c_int, [_ptr, _i64, _i32, _i32, _ptr, _ptr, _ptr]),
+    "sb_dsd_combine": (
+        _c_int,
+        [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr,
+         _ptr],
+    ),
     "sb_token_rounding": (
         _c_int,
         [_ptr, _i64, _i32, _i32, _i32, _i32, _i32, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,

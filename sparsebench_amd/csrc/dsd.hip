@@ -357,6 +357,172 @@ int launch_dsd_persistent(const void* blocks, const void* w, const int32_t* row_
   return check_launch("dsd");
 }
 
+// ---- DSD with the combine fused into its epilogue (top-k routing) --------
+//
+// out[t, :] = bf16( sum_j fp32(y[copy_row[t*k+j], :]) * fp32(gate[t*k+j]) ),
+// the combine of moe_forward, done by the tile that completes token t:
+// every tile writes its rows of y, publishes them (release fence, agent
+// scope: the XCDs' L2s are not coherent with each other), then counts each
+// of its tokens in on counters[t][column slice]. The tile whose count
+// completes a token (all its routed copies written for this slice) resets
+// the counter, takes an acquire fence and sums the token's rows in slot
+// order j, the order of combine_kernel, so the result is bit-identical to
+// the unfused path and independent of timing. No tile waits on another.
+// Extra workgroups past the tiles write zeros for tokens none of whose
+// copies was routed (bad expert ids), as the unfused combine does.
+template <typename G>
+__device__ __forceinline__ float gate_value(const G* g, int64_t i);
+template <>
+__device__ __forceinline__ float gate_value<uint16_t>(const uint16_t* g, int64_t i) {
+  return bf16_to_f32(g[i]);
+}
+template <>
+__device__ __forceinline__ float gate_value<_Float16>(const _Float16* g, int64_t i) {
+  return static_cast<float>(g[i]);
+}
+template <>
+__device__ __forceinline__ float gate_value<float>(const float* g, int64_t i) {
+  return g[i];
+}
+
+constexpr int kOrphanTokensPerGroup = 1024;
+
+template <class Cfg, typename G>
+__global__ void __launch_bounds__(Cfg::kThreads)
+    dsd_combine_kernel(const uint16_t* __restrict__ blocks, const uint16_t* __restrict__ w,
+                       const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ col_indices,
+                       const int32_t* __restrict__ row_token, const int32_t* __restrict__ copy_row,
+                       const G* __restrict__ gates, uint16_t* y, uint16_t* __restrict__ out,
+                       int32_t* __restrict__ counters, int64_t nnz, int64_t w_rows, int32_t num_row_blocks,
+                       int32_t d_model, int32_t num_slices, int32_t num_tokens, int32_t k,
+                       const int32_t* __restrict__ valid_tokens, int32_t num_tile_groups, int32_t group) {
+  using ML = DmaMainloop<Cfg>;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN;
+  constexpr int kChunksPerRow = BN / 8;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsAlloc];
+  // Tokens this tile completes, in the part of LDS the staged tile leaves free.
+  static_assert(Cfg::kLdsAlloc >= ML::kStagedBytes + (BM + 1) * 4, "room for the finish list");
+  int32_t* finish_token = reinterpret_cast<int32_t*>(lds + ML::kStagedBytes);
+  int32_t& num_finish = finish_token[BM];
+  const int tid = threadIdx.x;
+  const int32_t limit = valid_tokens ? min(num_tokens, *valid_tokens) : num_tokens;
+
+  if (static_cast<int32_t>(blockIdx.x) >= num_tile_groups) {
+    // Tokens with no routed copy: a zero row, as the unfused combine writes.
+    const int64_t base = static_cast<int64_t>(blockIdx.x - num_tile_groups) * kOrphanTokensPerGroup;
+    for (int64_t t = base + tid; t < base + kOrphanTokensPerGroup && t < limit; t += Cfg::kThreads) {
+      bool any = false;
+      for (int32_t j = 0; j < k; ++j) any = any || copy_row[t * k + j] >= 0;
+      if (!any)
+        for (int32_t c = 0; c < d_model; c += 8)
+          *reinterpret_cast<u32x4_t*>(out + t * d_model + c) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+
+  const int live_rb = live_row_blocks(row_offsets, num_row_blocks);
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
+  int rb, slice;
+  tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
+  const int n0 = slice * BN;
+  int32_t begin = row_offsets[rb];
+  int32_t end = row_offsets[rb + 1];
+  if (begin < 0 || end > nnz || end < begin) begin = end = 0;
+  if (begin == end) return;  // dead row block: holds no copy
+
+  DsdDmaSrc<Cfg> src;
+  src.blocks = blocks;
+  src.w = w + n0;
+  src.col_indices = col_indices;
+  src.w_rows = w_rows;
+  src.d_model = d_model;
+  src.begin = begin;
+  const ADmaPos<Cfg> ap;
+#pragma unroll
+  for (int q = 0; q < Cfg::kAInstr; ++q) src.a_off[q] = (ap.row[q] * BM + ap.chunk[q] * 8) * 2u;
+  const BDmaPos<Cfg> bp;
+#pragma unroll
+  for (int q = 0; q < Cfg::kBInstr; ++q)
+    src.b_off[q] = (static_cast<uint32_t>(bp.row[q]) * d_model + bp.col[q]) * 2u;
+
+  typename ML::Acc acc;
+  ML::run(lds, src, (end - begin) * DsdDmaSrc<Cfg>::kStepsPerBlock, acc);
+
+  uint16_t* y_tile = y + static_cast<int64_t>(rb) * BM * d_model + n0;
+  ML::stage_tile(lds, acc, [](float v) { return v; });
+  ML::for_each_staged_chunk(lds, [&](int r, int col, u32x4_t v) {
+    *reinterpret_cast<u32x4_t*>(y_tile + static_cast<int64_t>(r) * d_model + col) = v;
+  });
+
+  // Publish this tile's rows, then count its tokens in.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (tid == 0) num_finish = 0;
+  __syncthreads();
+  if (tid < BM) {
+    const int32_t t = row_token[static_cast<int64_t>(rb) * BM + tid];
+    if (t >= 0 && t < limit) {
+      int32_t routed = 0;
+      for (int32_t j = 0; j < k; ++j) routed += copy_row[static_cast<int64_t>(t) * k + j] >= 0 ? 1 : 0;
+      int32_t* ctr = counters + static_cast<int64_t>(t) * num_slices + slice;
+      const int32_t before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (before == routed - 1) {
+        __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next call
+        finish_token[atomicAdd(&num_finish, 1)] = t;
+      }
+    }
+  }
+  __syncthreads();
+  const int32_t nf = num_finish;
+  if (nf == 0) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (int q = tid; q < nf * kChunksPerRow; q += Cfg::kThreads) {
+    const int32_t t = finish_token[q / kChunksPerRow];
+    const int col = n0 + (q % kChunksPerRow) * 8;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int32_t j = 0; j < k; ++j) {
+      const int64_t c = static_cast<int64_t>(t) * k + j;
+      const int32_t row = copy_row[c];
+      if (row < 0) continue;
+      const float g = gate_value(gates, c);
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(y + static_cast<int64_t>(row) * d_model + col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[2 * e] += __uint_as_float(v[e] << 16) * g;
+        a[2 * e + 1] += __uint_as_float(v[e] & 0xffff0000u) * g;
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(out + static_cast<int64_t>(t) * d_model + col) =
+        u32x4_t{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(a[4], a[5]), pack_bf16x2(a[6], a[7])};
+  }
+}
+
+template <class Cfg, typename G>
+int launch_dsd_combine(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices,
+                       const int32_t* row_token, const int32_t* copy_row, const void* gates, void* y, void* out,
+                       int32_t* counters, int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t d_model,
+                       int64_t num_tokens, int32_t k, const int32_t* valid_tokens, hipStream_t stream) {
+  if (d_model % Cfg::BN != 0) return fail(SB_ERR_INVALID, "dsd: D %% tile width != 0");
+  const int32_t num_slices = static_cast<int32_t>(d_model / Cfg::BN);
+  const int64_t tiles = num_row_blocks * num_slices;
+  const int64_t orphan_groups = (num_tokens + kOrphanTokensPerGroup - 1) / kOrphanTokensPerGroup;
+  dsd_combine_kernel<Cfg, G><<<static_cast<uint32_t>(tiles + orphan_groups), Cfg::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(blocks), static_cast<const uint16_t*>(w), row_offsets, col_indices, row_token,
+      copy_row, static_cast<const G*>(gates), static_cast<uint16_t*>(y), static_cast<uint16_t*>(out), counters, nnz,
+      w_rows, static_cast<int32_t>(num_row_blocks), static_cast<int32_t>(d_model), num_slices,
+      static_cast<int32_t>(num_tokens), k, valid_tokens, static_cast<int32_t>(tiles), tile_group());
+  return check_launch("dsd+combine");
+}
+
+template <typename G, class... Args>
+int dispatch_dsd_combine(int variant, Args... args) {
+  switch (variant) {
+    case 25: return launch_dsd_combine<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2>, G>(args...);
+    case 32: return launch_dsd_combine<DmaCfg<128, 512, 32, 4, 1, 4, 0, 2>, G>(args...);
+    case 58: return launch_dsd_combine<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 1>, G>(args...);
+    default: return fail(SB_ERR_INVALID, "dsd+combine: unknown tile variant %d", variant);
+  }
+}
+
 template <class Cfg>
 int launch_dsd_dma(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices,
                    void* out, int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t d_model,
@@ -526,4 +692,46 @@ extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offs
                              zero_dead_rows, s);
   return dispatch_dsd<64>(variant, blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
                           zero_dead_rows, s);
+}
+
+extern "C" int sb_dsd_combine(const void* blocks, const void* w, const int32_t* row_offsets,
+                              const int32_t* col_indices, const int32_t* row_token, const int32_t* copy_row,
+                              const void* gates, int32_t gate_dtype, void* y, void* out, int32_t* counters,
+                              int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t d_model,
+                              int64_t num_tokens, int32_t k, const int32_t* valid_tokens, void* stream) {
+  constexpr int64_t kI32Max = 2147483647;
+  if (d_model <= 0 || d_model % 256 != 0)
+    return fail(SB_ERR_INVALID, "dsd+combine needs D (%lld) to be a multiple of 256", static_cast<long long>(d_model));
+  if (num_row_blocks < 0 || w_rows < 0 || w_rows % 128 != 0 || nnz < 0)
+    return fail(SB_ERR_INVALID, "dsd+combine: bad layout sizes");
+  if (num_tokens <= 0 || num_tokens > kI32Max / 8 || k <= 0 || num_tokens * k > kI32Max)
+    return fail(SB_ERR_INVALID, "dsd+combine: bad token count or k");
+  if (num_row_blocks * 128 > kI32Max || num_row_blocks * (d_model / 128) > kI32Max)
+    return fail(SB_ERR_INVALID, "dsd+combine: too many row blocks");
+  if (!blocks || !w || !row_offsets || !col_indices || !row_token || !copy_row || !gates || !y || !out || !counters)
+    return fail(SB_ERR_INVALID, "dsd+combine: null buffer");
+  if (!aligned16(blocks) || !aligned16(w) || !aligned16(y) || !aligned16(out))
+    return fail(SB_ERR_INVALID, "dsd+combine: blocks, w, y and out must be 16-byte aligned");
+  if (num_row_blocks == 0) return clear_ok();
+  const hipStream_t s = as_stream(stream);
+  const int forced = tuning_override("SPARSEBENCH_DSD_VARIANT");
+  const int64_t row_k = nnz / num_row_blocks * 128;
+  int variant = forced == 25 || forced == 32 || forced == 58 ? forced : (row_k >= 8192 ? 25 : row_k < 2048 ? 58 : 32);
+  if (d_model % 512 != 0 && variant != 25) variant = 25;
+  switch (gate_dtype) {
+    case SB_DTYPE_BF16:
+      return dispatch_dsd_combine<uint16_t>(variant, blocks, w, row_offsets, col_indices, row_token, copy_row, gates,
+                                            y, out, counters, nnz, w_rows, num_row_blocks, d_model, num_tokens, k,
+                                            valid_tokens, s);
+    case SB_DTYPE_F16:
+      return dispatch_dsd_combine<_Float16>(variant, blocks, w, row_offsets, col_indices, row_token, copy_row, gates,
+                                            y, out, counters, nnz, w_rows, num_row_blocks, d_model, num_tokens, k,
+                                            valid_tokens, s);
+    case SB_DTYPE_F32:
+      return dispatch_dsd_combine<float>(variant, blocks, w, row_offsets, col_indices, row_token, copy_row, gates, y,
+                                         out, counters, nnz, w_rows, num_row_blocks, d_model, num_tokens, k,
+                                         valid_tokens, s);
+    default:
+      return fail(SB_ERR_INVALID, "dsd+combine: unsupported gate dtype code %d", gate_dtype);
+  }
 }

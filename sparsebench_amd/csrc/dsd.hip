@@ -519,6 +519,9 @@ int dispatch_dsd_combine(int variant, Args... args) {
     case 25: return launch_dsd_combine<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2>, G>(args...);
     case 32: return launch_dsd_combine<DmaCfg<128, 512, 32, 4, 1, 4, 0, 2>, G>(args...);
     case 58: return launch_dsd_combine<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 1>, G>(args...);
+    case 62: return launch_dsd_combine<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 3>, G>(args...);
+    case 63: return launch_dsd_combine<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 3>, G>(args...);
+    case 64: return launch_dsd_combine<DmaCfg<128, 512, 32, 4, 1, 4, 0, 2, 3>, G>(args...);
     default: return fail(SB_ERR_INVALID, "dsd+combine: unknown tile variant %d", variant);
   }
 }
@@ -623,6 +626,20 @@ int dispatch_dsd(int variant, Args... args) {
     case 59:
       if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 64, 2, 2, 4, 0, 2, 2>>(args...);
       else return launch_dsd_dma<DmaCfg<BM, 512, 64, 2, 1, 4, 0, 2, 2>>(args...);
+    // The next step's DMA interleaved with the MFMAs (PIPE 3).
+    case 61:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 64, 2, 2, 4, 0, 2, 3>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 512, 64, 2, 1, 4, 0, 2, 3>>(args...);
+    case 62:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 2, 4, 0, 2, 3>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 3>>(args...);
+    case 63:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 4, 0, 2, 3>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 256, 64, 3, 2, 2, 0, 2, 3>>(args...);
+    case 64: return launch_dsd_dma<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 3>>(args...);
+    case 65:
+      if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 512, 32, 3, 2, 4, 0, 2, 3>>(args...);
+      else return launch_dsd_dma<DmaCfg<BM, 512, 32, 3, 1, 4, 0, 2, 3>>(args...);
     case 37:
       if constexpr (BM == 128) return launch_dsd_dma<DmaCfg<BM, 256, 32, 6, 2, 4, 0, 2>>(args...);
       else return launch_dsd_dma<DmaCfg<BM, 256, 32, 6, 2, 2, 0, 2>>(args...);
@@ -670,23 +687,25 @@ extern "C" int sb_dsd(const void* blocks, const void* w, const int32_t* row_offs
   const hipStream_t s = as_stream(stream);
   const int forced = tuning_override("SPARSEBENCH_DSD_VARIANT");
   // Default, from timing every variant on the benchmark shapes (MI355X,
-  // samples interleaved across variants): 128 x 512 tiles, 4 waves of
-  // 128 x 128, BK 32 x 4-stage LDS-DMA ring with non-temporal W loads. The
-  // row's reduction depth (K = F per expert, read from the buffer shape:
-  // nnz / num_row_blocks blocks per row) moves the choice: with K >= 8192
-  // (few row blocks, so few wide tiles per CU) 128 x 256 tiles of 8 waves;
-  // with K < 2048 (short tiles) 128 x 512 tiles of 8 waves of 64 x 128.
+  // samples interleaved across variants): 128 x 512 tiles, BK 32 x 4-stage
+  // LDS-DMA ring with non-temporal W loads, the next stage's DMA and the
+  // next sub-step's fragment reads issued among the MFMAs; 4 waves of
+  // 128 x 128. With a deep reduction (K = F per expert >= 8192, read from
+  // the buffer shape: nnz / num_row_blocks blocks per row) 8 waves of
+  // 64 x 128.
   const int64_t row_k = num_row_blocks > 0 ? nnz / num_row_blocks * block_size : 0;
-  int variant = forced > 0 ? forced : (row_k >= 8192 ? 25 : row_k < 2048 ? 58 : 32);
+  int variant = forced > 0 ? forced : (row_k >= 8192 ? 62 : 64);
   if (d_model % 256 != 0 && (variant == 2 || variant == 4 || variant == 5 || variant == 6 || variant == 14 ||
                              variant == 15 || variant == 16 || variant == 17 || variant == 24 || variant == 25 ||
                              variant == 26 || variant == 34 || variant == 35 || variant == 36 || variant == 37 ||
                              variant == 38 || variant == 41 || variant == 44 || variant == 51 || variant == 53 ||
-                             variant == 54))
+                             variant == 54 || variant == 63))
     variant = 1;
   if (d_model % 512 != 0 &&
       ((variant >= 31 && variant <= 33) || variant == 42 || variant == 52 || (variant >= 55 && variant <= 59)))
     variant = d_model % 256 == 0 ? 25 : 21;
+  if (d_model % 512 != 0 && (variant == 61 || variant == 62 || variant == 64 || variant == 65))
+    variant = d_model % 256 == 0 ? 63 : 21;
   if (block_size == 128)
     return dispatch_dsd<128>(variant, blocks, w, row_offsets, col_indices, out, nnz, w_rows, num_row_blocks, d_model,
                              zero_dead_rows, s);
@@ -716,8 +735,10 @@ extern "C" int sb_dsd_combine(const void* blocks, const void* w, const int32_t* 
   const hipStream_t s = as_stream(stream);
   const int forced = tuning_override("SPARSEBENCH_DSD_VARIANT");
   const int64_t row_k = nnz / num_row_blocks * 128;
-  int variant = forced == 25 || forced == 32 || forced == 58 ? forced : (row_k >= 8192 ? 25 : row_k < 2048 ? 58 : 32);
-  if (d_model % 512 != 0 && variant != 25) variant = 25;
+  int variant = forced == 25 || forced == 32 || forced == 58 || forced == 62 || forced == 63 || forced == 64
+                    ? forced
+                    : (row_k >= 8192 ? 62 : 64);
+  if (d_model % 512 != 0 && variant != 25 && variant != 63) variant = 63;
   switch (gate_dtype) {
     case SB_DTYPE_BF16:
       return dispatch_dsd_combine<uint16_t>(variant, blocks, w, row_offsets, col_indices, row_token, copy_row, gates,

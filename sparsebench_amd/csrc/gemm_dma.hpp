@@ -28,6 +28,8 @@
 // Both sides hold k = 8 (lane / 32) + 0..7 of the 16-step, in the same order.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace sb {
@@ -65,7 +67,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // its fragments then run its MFMAs (the compiler schedules). 1: two
 // fragment register sets, sub-step s+1's LDS reads issued among sub-step
 // s's MFMAs (scheduling groups pin the interleave). 2: the two register
-// sets without the pinned interleave.
+// sets without the pinned interleave. 3: as 1, and the DMA of the step
+// STAGES-1 ahead is issued among the MFMAs too, not as a burst after the
+// barrier (a burst of DMA instructions holds each wave at issue until the
+// address unit takes them, which delays its MFMAs).
 template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0, int PIPE_ = 0>
 struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_;
@@ -156,6 +161,32 @@ __device__ __forceinline__ void sched_interleave() {
   }
 }
 
+// f(integral_constant<int, I>) for I = B .. E-1, in order.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// PIPE 3 scheduling groups for one sub-step of kMfma MFMAs: after MFMA Q
+// come up to kPer of the next sub-step's kReads DS reads, and the DMA
+// instructions whose turn it is, kDma of them spread evenly over the MFMAs
+// (masks: 0x008 MFMA, 0x100 DS read, 0x020 VMEM read).
+template <int Q, int kMfma, int kReads, int kPer, int kDma>
+__device__ __forceinline__ void sched_substep_with_dma() {
+  if constexpr (Q < kMfma) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int left = kReads - Q * kPer;
+    constexpr int n = left <= 0 ? 0 : (left < kPer ? left : kPer);
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+    constexpr int due = (Q + 1) * kDma / kMfma - Q * kDma / kMfma;
+    if constexpr (due > 0) __builtin_amdgcn_sched_group_barrier(0x020, due, 0);
+    sched_substep_with_dma<Q + 1, kMfma, kReads, kPer, kDma>();
+  }
+}
+
 // s_waitcnt vmcnt(later * L) for a run-time `later` in [0, MAXL].
 template <int L, int MAXL>
 __device__ __forceinline__ void wait_steps(int later) {
@@ -180,30 +211,56 @@ struct DmaMainloop {
   // reads, and saying so lets the compiler drop the vmcnt(0) it would
   // otherwise put before every LDS read (which serializes loads and MFMAs).
   // The DMA of K step `t` of `src` into ring slot `ring % STAGES`.
+  // The DMA instructions of one K step: dma(q), q < kLoadsPerStep, issues
+  // this wave's instruction q (A rows first, then B rows).
   template <class Src>
-  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int ring, int t, const Src& src) {
-    const int wave = threadIdx.x >> 6;
-    uint8_t* stage = lds + (ring % Cfg::STAGES) * Cfg::kStageBytes;
+  struct StepDma {
+    uint8_t* __restrict__ stage;
     __amdgpu_buffer_rsrc_t ra, rb;
     uint32_t sa, sb;
-    src.a_src(t, &ra, &sa);
-    src.b_src(t, &rb, &sb);
-    // The scalar offsets are uniform by contract; saying so keeps the
-    // compiler from wrapping each load in a per-lane waterfall loop when it
-    // cannot prove it.
-    sa = __builtin_amdgcn_readfirstlane(sa);
-    sb = __builtin_amdgcn_readfirstlane(sb);
+    const Src& src;
+    int wave;
+    __device__ __forceinline__ StepDma(uint8_t* __restrict__ stage_, int t, const Src& src_) : stage(stage_), src(src_) {
+      wave = threadIdx.x >> 6;
+      src.a_src(t, &ra, &sa);
+      src.b_src(t, &rb, &sb);
+      // The scalar offsets are uniform by contract; saying so keeps the
+      // compiler from wrapping each load in a per-lane waterfall loop when
+      // it cannot prove it.
+      sa = __builtin_amdgcn_readfirstlane(sa);
+      sb = __builtin_amdgcn_readfirstlane(sb);
+    }
+    __device__ __forceinline__ void operator()(int q) const {
+      if (q < Cfg::kAInstr)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024), 16,
+                                                 src.a_voff(q), sa, 0, Cfg::CPA);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q - Cfg::kAInstr) * 1024), 16,
+            src.b_voff(q - Cfg::kAInstr), sb, 0, Cfg::CPB);
+    }
+  };
+
+  template <class Src>
+  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int ring, int t, const Src& src) {
+    const StepDma<Src> dma(lds + (ring % Cfg::STAGES) * Cfg::kStageBytes, t, src);
 #pragma unroll
-    for (int q = 0; q < Cfg::kAInstr; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024), 16,
-                                               src.a_voff(q), sa, 0, Cfg::CPA);
-#pragma unroll
-    for (int q = 0; q < Cfg::kBInstr; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q) * 1024), 16, src.b_voff(q), sb, 0, Cfg::CPB);
+    for (int q = 0; q < Cfg::kLoadsPerStep; ++q) dma(q);
   }
 
+  struct NoDma {
+    __device__ __forceinline__ void operator()(int) const {}
+  };
+
   __device__ __forceinline__ static void compute(const uint8_t* __restrict__ stage, Acc& acc) {
+    compute(stage, acc, NoDma{});
+  }
+
+  // One K step's fragments and MFMAs. With PIPE 3, dma(q) for q <
+  // kLoadsPerStep is called among the MFMAs (a later step's loads, into
+  // another stage), spread evenly by the scheduling groups.
+  template <class Dma>
+  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ stage, Acc& acc, const Dma& dma) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     const int h = lane >> 5;
@@ -251,6 +308,33 @@ struct DmaMainloop {
         for (int i = 0; i < Cfg::TM; ++i)
           acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[jn], a[i], acc[jn][i], 0, 0, 0);
     };
+    if constexpr (Cfg::PIPE == 3) {
+      constexpr int kMfma = Cfg::TM * Cfg::TN;
+      constexpr int kReads = Cfg::TM + 2 * Cfg::TN;
+      constexpr int kPer = (kReads + kMfma - 1) / kMfma;
+      constexpr int kDma = __is_same(Dma, NoDma) ? 0 : Cfg::kLoadsPerStep;
+      bf16x8_t a[2][Cfg::TM], b[2][Cfg::TN];
+      read_a(0, a[0]);
+      read_b(0, b[0]);
+      // Each sub-step is its own scheduling region (sched_barrier), holding
+      // its MFMAs, the next sub-step's fragment reads and its share of the
+      // DMA instructions, so the DMA spreads over the whole step.
+      static_for<0, kSub>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        if constexpr (s + 1 < kSub) {
+          read_a(s + 1, a[(s + 1) & 1]);
+          read_b(s + 1, b[(s + 1) & 1]);
+        }
+        mfmas(a[s & 1], b[s & 1]);
+#pragma unroll
+        for (int q = s * kDma / kSub; q < (s + 1) * kDma / kSub; ++q) dma(q);
+        if constexpr (s == 0) __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // sub-step 0's own reads
+        sched_substep_with_dma<0, kMfma, (s + 1 < kSub ? kReads : 0), kPer,
+                               (s + 1) * kDma / kSub - s * kDma / kSub>();
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      return;
+    }
     if constexpr (Cfg::PIPE == 0) {
 #pragma unroll
       for (int s = 0; s < kSub; ++s) {
@@ -299,6 +383,25 @@ struct DmaMainloop {
 #pragma unroll
     for (int s = 0; s < Cfg::STAGES - 1; ++s)
       if (s < num_steps) issue(lds, s, s, src);
+    if constexpr (Cfg::PIPE == 3) {
+      // Steps that issue a later step's loads, among their MFMAs; at the top
+      // of each, steps t .. t+STAGES-2 are outstanding.
+      int t = 0;
+      for (; t + Cfg::STAGES - 1 < num_steps; ++t) {
+        wait_vmcnt<(Cfg::STAGES - 2) * Cfg::kLoadsPerStep>();
+        __builtin_amdgcn_s_barrier();
+        const int u = t + Cfg::STAGES - 1;
+        compute(lds + (t % Cfg::STAGES) * Cfg::kStageBytes, acc,
+                StepDma<Src>(lds + (u % Cfg::STAGES) * Cfg::kStageBytes, u, src));
+      }
+      // The last STAGES-1 steps issue nothing.
+      for (; t < num_steps; ++t) {
+        wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(num_steps - 1 - t);
+        __builtin_amdgcn_s_barrier();
+        compute(lds + (t % Cfg::STAGES) * Cfg::kStageBytes, acc);
+      }
+      return;
+    }
     for (int t = 0; t < num_steps; ++t) {
       // Step t's loads are complete once at most the later issued steps
       // (t+1 .. t+STAGES-2, if they exist) are outstanding.

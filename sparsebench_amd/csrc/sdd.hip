@@ -486,6 +486,12 @@ int dispatch_sdd(int variant, Args... args) {
     case 57: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 2>, kFastGelu>(args...);
     case 58: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 1>, kFastGelu>(args...);
     case 59: return launch_sdd_dma<DmaCfg<128, 512, 64, 2, 2, 4, 0, 2, 2>, kFastGelu>(args...);
+    // The next step's DMA interleaved with the MFMAs (PIPE 3).
+    case 61: return launch_sdd_dma<DmaCfg<128, 512, 64, 2, 2, 4, 0, 2, 3>, kFastGelu>(args...);
+    case 62: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 3>, kFastGelu>(args...);
+    case 63: return launch_sdd_dma<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 3>, kFastGelu>(args...);
+    case 64: return launch_sdd_dma<DmaCfg<128, 512, 32, 4, 1, 4, 0, 2, 3>, kFastGelu>(args...);
+    case 65: return launch_sdd_dma<DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3>, kFastGelu>(args...);
     case 41: return launch_sdd_persistent<DmaCfg<128, 256, 64, 3, 2, 4, 0, 2>, kFastGelu>(args...);
     case 43: return launch_sdd_persistent<DmaCfg<128, 128, 64, 2, 2, 2, 0, 2>, kFastGelu>(args...);
     case 44: return launch_sdd_persistent<DmaCfg<128, 256, 32, 3, 2, 4, 0, 2>, kFastGelu>(args...);
@@ -526,13 +532,15 @@ extern "C" int sb_sdd(const void* x, const void* w1, const int32_t* row_token, c
   // Default, from timing every variant on the benchmark shapes (MI355X,
   // samples interleaved across variants): 128 x 512 tiles of 8 waves, each
   // 64 x 128 (8 MFMAs per 16-deep sub-step: enough work to cover the LDS
-  // fragment reads, 2 waves per SIMD), non-temporal weight loads; a 2-stage
-  // BK 64 ring, or with a deep reduction (D >= 4096) a 4-stage BK 32 ring
-  // with the fragment reads of the next sub-step interleaved. F must be a
-  // multiple of 512; otherwise 128 x 256 tiles of 8 waves.
-  int variant = forced > 0 ? forced : (d_model >= 4096 ? 58 : 59);
+  // fragment reads, 2 waves per SIMD), non-temporal weight loads, BK 32,
+  // the next stage's DMA and the next sub-step's fragment reads issued
+  // among the MFMAs; a 3-stage ring, or with a deep reduction (D >= 4096) a
+  // 4-stage one. F must be a multiple of 512; otherwise 128 x 256 tiles of
+  // 8 waves, BK 64 x 3 stages.
+  int variant = forced > 0 ? forced : (d_model >= 4096 ? 62 : 65);
   if (ffn_dim % 512 != 0 && ((variant >= 31 && variant <= 33) || variant == 52 || (variant >= 55 && variant <= 59)))
     variant = 25;
+  if (ffn_dim % 512 != 0 && (variant == 61 || variant == 62 || variant == 64 || variant == 65)) variant = 63;
   if (gelu_mode > 0)
     return dispatch_sdd<false>(variant, x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model,
                                ffn_dim, num_experts, num_row_blocks, apply_gelu, s);

@@ -81,3 +81,14 @@ def test_fused_valid_tokens_and_graph_replay() -> None:
         torch.cuda.synchronize()
         ref = moe_forward(x, idx, gates, w1, w2, valid_tokens=valid)
         assert torch.equal(out[:t], ref[:t])
+
+
+@pytest.mark.parametrize("variant", [25, 32, 58, 62, 63, 64])
+def test_fused_every_tile_form(variant, monkeypatch) -> None:
+    from sparsebench_amd.moe import moe_forward
+
+    x, idx, gates, w1, w2 = make(1500, 16, 1024, 512, "zipf", seed=11)
+    ref = moe_forward(x, idx, gates, w1, w2)
+    monkeypatch.setenv("SPARSEBENCH_DSD_VARIANT", str(variant))
+    assert torch.equal(moe_forward(x, idx, gates, w1, w2, fused_combine=True), ref)
+    assert torch.equal(moe_forward(x, idx, gates, w1, w2, fused_combine=True), ref)

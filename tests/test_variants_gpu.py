@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = {"rtol": 1.6e-2, "atol": 1.6e-2}
 COMMON = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 21, 22, 23, 24, 25, 26, 27, 31, 32, 33, 34,
-          35, 36, 37, 38, 39, 51, 52, 53, 54, 55, 56, 57, 58, 59]
+          35, 36, 37, 38, 39, 51, 52, 53, 54, 55, 56, 57, 58, 59, 61, 62, 63, 64, 65]
 SDD_PERSISTENT = [41, 43, 44]
 DSD_PERSISTENT = [41, 42, 43, 44, 45]
 SDD_VARIANTS = COMMON + SDD_PERSISTENT

@@ -159,6 +159,9 @@ __global__ void __launch_bounds__(256)
                             const G* __restrict__ weights, const int32_t* __restrict__ offsets,
                             const int32_t* __restrict__ copies, uint16_t* __restrict__ out, int64_t num_tokens,
                             int32_t chunks_per_row, int64_t y_rows, const int32_t* __restrict__ valid_tokens) {
+  // Products rounded, then added (no fused multiply-add), as the reference's
+  // index_add_ of rows.float() * weight.
+#pragma clang fp contract(off)
   const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t t = item / chunks_per_row;
   const int32_t ch = static_cast<int32_t>(item % chunks_per_row);

@@ -476,6 +476,7 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   if (nf == 0) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   for (int q = tid; q < nf * kChunksPerRow; q += Cfg::kThreads) {
+#pragma clang fp contract(off)  // as sb_combine: products rounded, then added
     const int32_t t = finish_token[q / kChunksPerRow];
     const int col = n0 + (q % kChunksPerRow) * 8;
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};

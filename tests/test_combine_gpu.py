@@ -5,6 +5,7 @@ after its fp32 sum, so the two agree to one bf16 rounding step plus fp32
 summation order: rtol 1e-2, atol 1e-5.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -27,7 +28,8 @@ def make(num_tokens: int, k: int, d_model: int, rows: int, gate_dtype, seed: int
 
 
 @pytest.mark.parametrize("gate_dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize(("num_tokens", "k", "d_model"), [(1, 1, 8), (300, 2, 256), (77, 4, 1024), (4096, 2, 1024)])
+@pytest.mark.parametrize(("num_tokens", "k", "d_model"),
+                         [(1, 1, 8), (300, 2, 256), (77, 4, 1024), (4096, 2, 1024), (50, 3, 64), (33, 8, 128)])
 def test_matches_closed_form(gate_dtype, num_tokens, k, d_model) -> None:
     from sparsebench_amd.moe import combine
 
@@ -69,3 +71,35 @@ def test_valid_tokens_stops_at_the_device_count() -> None:
     torch.testing.assert_close(out[:40].float().cpu(), combine_reference(y, copy_row.numpy(), w)[:40], **TOL)
     full = _C.combine_cuda(y.cuda(), copy_row.cuda(), w.cuda())
     assert torch.equal(out[:40], full[:40])
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 8])
+def test_sums_in_slot_order_exactly(k) -> None:
+    # out = bf16(((0 + y0*g0) + y1*g1) + ...), fp32 throughout, skipped
+    # copies adding nothing: a sequential fp32 sum gives the same bits.
+    from sparsebench_amd.moe import combine
+
+    num_tokens, d_model = 200, 64
+    y, copy_row, w = make(num_tokens, k, d_model, num_tokens * k + 5, torch.float32, skipped=0.2)
+    out = combine(y.cuda(), copy_row.cuda(), w.cuda()).cpu()
+    yf = y.float().numpy()
+    rows = copy_row.numpy().reshape(num_tokens, k)
+    wf = w.float().numpy()
+    acc = np.zeros((num_tokens, d_model), dtype=np.float32)
+    for j in range(k):
+        r = rows[:, j]
+        ok = r >= 0
+        acc[ok] = (acc[ok] + yf[r[ok]] * wf[ok, j][:, None]).astype(np.float32)
+    assert torch.equal(out, torch.from_numpy(acc).bfloat16())
+
+
+@pytest.mark.parametrize("gate_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("k", [1, 2])
+def test_bit_exact_to_reference_arithmetic(gate_dtype, k) -> None:
+    # With at most two products the reference's .sum() has one order, so
+    # rounded products then one fp32 add must give the oracle's bits exactly.
+    from sparsebench_amd.moe import combine
+
+    y, copy_row, w = make(1000, k, 512, 1000 * k + 9, gate_dtype, seed=4, skipped=0.1)
+    out = combine(y.cuda(), copy_row.cuda(), w.cuda()).cpu()
+    assert torch.equal(out, combine_reference(y, copy_row.numpy(), w).bfloat16())

@@ -3,7 +3,7 @@ computing it on the same MI355X (the measurements of the reference's
 bench/bench_moe.py and bench/bench_token_rounding.py, made here).
 
     python bench_baselines.py                 # both tables, markdown on stdout
-    python bench_baselines.py --only layer    # or: --only rounding
+    python bench_baselines.py --only layer    # or: --only rounding, --only ceilings
 
 Layer pipelines (everything from the routing to the [T, D] output is timed,
 host syncs included):
@@ -21,6 +21,11 @@ Token rounding (SonicMoE; the router's scores from workloads.router_scores):
   moe_forward_assigned and for the grouped_mm pipeline on the same list; the
   rounding step alone (routing.route_rounded: rounding, its list and its
   layout, no sync); and moe_forward_rounded (rounding fused into the layer).
+
+Ceilings (the box's practical roofs, next to the published 8 TB/s and
+2.5 PFLOP/s): streaming reads of 2 GiB with 16-byte vector loads and through
+LDS DMA (sb_read_probe, the load path of SDD / DSD), a 1 GiB device copy, and
+dense bf16 GEMMs through torch.matmul (hipBLASLt).
 
 Every pipeline is checked against the fp32 loop reference before it is
 timed (max error <= 3e-2 (1 + max |ref|), the reference's check). Timing: a
@@ -197,9 +202,39 @@ def rounding_table(flush: torch.Tensor) -> list[str]:
     return lines
 
 
+def ceilings_table(flush: torch.Tensor) -> list[str]:
+    from sparsebench_amd import _C
+
+    lines = ["| measurement | ms | rate | of published peak |", "|---|---:|---:|---:|"]
+    print("\n".join(lines), flush=True)
+    data = torch.ones(2 << 30, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    for mode in ("vector", "lds_dma"):
+        ms = time_ms(lambda: _C.read_probe(data, mode, sink), flush)
+        tbs = data.numel() / ms / 1e9
+        lines.append(f"| read 2 GiB, {mode} | {ms:.3f} | {tbs:.2f} TB/s | {tbs / 8.0:.0%} |")
+        print(lines[-1], flush=True)
+    src, dst = data[: 1 << 30], data[1 << 30:]
+    ms = time_ms(lambda: dst.copy_(src), flush)
+    tbs = 2 * src.numel() / ms / 1e9
+    lines.append(f"| copy 1 GiB (read + write) | {ms:.3f} | {tbs:.2f} TB/s | {tbs / 8.0:.0%} |")
+    print(lines[-1], flush=True)
+    del data, src, dst
+    torch.cuda.empty_cache()
+    for m, n, k in ((8192, 8192, 8192), (8192, 14336, 4096), (8192, 4096, 14336)):
+        a = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(k, n, device="cuda", dtype=torch.bfloat16)
+        ms = time_ms(lambda: a @ b, flush)
+        tf = 2 * m * n * k / ms / 1e9
+        lines.append(f"| bf16 GEMM {m}x{n}x{k} (torch.matmul) | {ms:.3f} | {tf:.0f} TFLOP/s | {tf / 2500:.0%} |")
+        print(lines[-1], flush=True)
+        del a, b
+    return lines
+
+
 def main() -> None:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("--only", choices=["layer", "rounding"])
+    p.add_argument("--only", choices=["layer", "rounding", "ceilings"])
     args = p.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit("bench_baselines.py needs a GPU")
@@ -212,6 +247,10 @@ def main() -> None:
     if args.only in (None, "rounding"):
         print("## Token rounding (tile 128, top-2)\n", flush=True)
         rounding_table(flush)
+        print(flush=True)
+    if args.only in (None, "ceilings"):
+        print("## Ceilings of this box\n", flush=True)
+        ceilings_table(flush)
 
 
 if __name__ == "__main__":

@@ -41,6 +41,14 @@ int32_t sb_version(void);
  * into out[0..n). n must be positive. */
 int sb_arch_probe(int32_t* out, int64_t n, void* stream);
 
+/* No counterpart in the reference: a measurement aid for the roofline.
+ * Reads bytes of device memory at data (16-byte aligned) once, mode 0 with
+ * 16-byte vector loads over a grid of 8 workgroups per CU, mode 1 through
+ * LDS DMA (buffer_load ... lds) as the SDD / DSD main loops read, one
+ * workgroup per MiB (bytes a multiple of 1 MiB). What is read is folded
+ * into one word per lane, stored to sink[0..256) only if it equals key. */
+int sb_read_probe(const void* data, int64_t bytes, int32_t mode, uint32_t key, uint32_t* sink, void* stream);
+
 /* Worst-case sizes of the routing outputs for n = T*k copies
  * (csrc/routing.cu:306-311). Host-only arithmetic; returns SB_ERR_INVALID
  * when the problem does not fit int32 indexing. */

@@ -54,6 +54,23 @@ def arch_probe(n: int) -> torch.Tensor:
     return out
 
 
+READ_PROBE_MODES = {"vector": 0, "lds_dma": 1}
+
+
+def read_probe(data: torch.Tensor, mode: str, sink: torch.Tensor) -> None:
+    """Read all of `data` once on the device (a bandwidth probe; see
+    sb_read_probe): mode "vector" (16-byte loads) or "lds_dma" (whole MiB)."""
+    if not data.is_cuda or not data.is_contiguous():
+        _fail("read_probe: data must be a contiguous CUDA tensor")
+    if mode not in READ_PROBE_MODES:
+        _fail(f"read_probe: mode must be one of {sorted(READ_PROBE_MODES)}, got {mode!r}")
+    if sink.dtype != torch.int32 or sink.numel() < 256 or not sink.is_cuda:
+        _fail("read_probe: sink must be a CUDA int32 tensor of at least 256 elements")
+    nbytes = data.numel() * data.element_size()
+    check(lib().sb_read_probe(data.data_ptr(), nbytes, READ_PROBE_MODES[mode], 0x9E3779B9, sink.data_ptr(),
+                              stream_of(data.device)))
+
+
 def routing_sizes(num_copies: int, num_experts: int, ffn_dim: int, block_size: int) -> tuple[int, int, int]:
     """(max_row_blocks, max_rows, workspace int32 elements) for n = T*k copies."""
     rb, rows, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()

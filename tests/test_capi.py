@@ -173,3 +173,16 @@ def test_dsd_combine_rejects(lib) -> None:
     assert "token count" in _err(lib)
     assert lib.sb_dsd_combine(*args, 7, p, p, p, 2, 128, 1, 256, 4, 2, None, None) == 1
     assert "gate dtype" in _err(lib)
+
+
+def test_read_probe_rejects(lib) -> None:
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
+    assert lib.sb_read_probe(p, 100, 0, 0, p, None) == 1
+    assert "multiple of 16" in _err(lib)
+    assert lib.sb_read_probe(p, 4096, 1, 0, p, None) == 1
+    assert "whole MiB" in _err(lib)
+    assert lib.sb_read_probe(p, 4096, 7, 0, p, None) == 1
+    assert "mode must be" in _err(lib)
+    assert lib.sb_read_probe(None, 4096, 0, 0, p, None) == 1
+    assert "null buffer" in _err(lib)

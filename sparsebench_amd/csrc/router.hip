@@ -16,8 +16,9 @@
 // The list is in (token, expert) order, like the reference's nonzero().
 //
 // Launches:
-//   1. topk      one wave per token: the k best experts (value, then lower
-//                index), per-chunk pick counts, the shifted scores stored
+//   1. topk      one lane per token (one wave per token when E x k is
+//                large): the k best experts (value, then lower index),
+//                per-chunk pick counts, the shifted scores stored
 //                expert-major, and (for top_k_assignments) the list itself.
 //   2. targets   one workgroup: counts -> targets -> padded_offsets.
 //   3. select    one workgroup per expert: radix select (4 passes of 8 bits)
@@ -173,6 +174,100 @@ __global__ void __launch_bounds__(kTopkThreads)
   if (chunk_counts != nullptr)
     for (int e = tid; e < num_experts; e += kTopkThreads)
       chunk_counts[static_cast<int64_t>(blockIdx.x) * num_experts + e] = hist[e];
+}
+
+// Top-k with one lane per token (a wave of 64 tokens per workgroup, the
+// same chunking as router_topk_kernel). The lane walks its token's row of
+// scores in expert order and keeps the KMAX best in registers, sorted by
+// (score desc, expert asc): each new (score, e) is bubbled in with
+// compare-and-swap steps, so an equal score behind an earlier expert stays
+// behind it. No lane talks to another, and the expert-major stores of the
+// shifted scores are 64 consecutive tokens per instruction. The outputs are
+// those of router_topk_kernel.
+template <int KMAX>
+__global__ void __launch_bounds__(64)
+    router_topk_lane_kernel(const float* __restrict__ scores, int64_t num_tokens, int32_t num_experts, int32_t k,
+                            float* __restrict__ shifted, int32_t* __restrict__ chunk_counts,
+                            int32_t* __restrict__ top_idx, float* __restrict__ top_weight) {
+  __shared__ int32_t hist[kMaxExperts];
+  __shared__ uint32_t picked_bits[64 * (kMaxExperts / 32)];  // lane-major: this lane's picks, one bit per expert
+  const int lane = threadIdx.x;
+  const int words = (num_experts + 31) / 32;
+  if (chunk_counts != nullptr)
+    for (int e = lane; e < num_experts; e += 64) hist[e] = 0;
+  for (int w = 0; w < words; ++w) picked_bits[lane * words + w] = 0u;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  const bool live = t < num_tokens;
+  const float* row = scores + (live ? t : 0) * num_experts;
+
+  float bv[KMAX];
+  int bi[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    bv[j] = 0.0f;
+    bi[j] = 0x7fffffff;  // empty
+  }
+  auto offer = [&](float v, int e) {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j < k && (bi[j] == 0x7fffffff || better(v, e, bv[j], bi[j]))) {
+        const float tv = bv[j];
+        const int ti = bi[j];
+        bv[j] = v;
+        bi[j] = e;
+        v = tv;
+        e = ti;
+      }
+    }
+  };
+  if (live) {
+    int e = 0;
+    if ((num_experts & 3) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15) == 0) {
+      // 16 scores (four 16-byte loads) in flight at a time.
+      for (; e + 16 <= num_experts; e += 16) {
+        float4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = *reinterpret_cast<const float4*>(row + e + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          offer(q[u].x, e + 4 * u);
+          offer(q[u].y, e + 4 * u + 1);
+          offer(q[u].z, e + 4 * u + 2);
+          offer(q[u].w, e + 4 * u + 3);
+        }
+      }
+    }
+    for (; e < num_experts; ++e) offer(row[e], e);
+  }
+  __syncthreads();  // hist and picked_bits cleared
+  if (live) {
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j < k && bi[j] != 0x7fffffff) {
+        total += bv[j];  // in pick order
+        picked_bits[lane * words + (bi[j] >> 5)] |= 1u << (bi[j] & 31);
+        if (chunk_counts != nullptr) atomicAdd(&hist[bi[j]], 1);
+        if (top_idx != nullptr) top_idx[t * k + j] = bi[j];
+      }
+    }
+    if (top_weight != nullptr)
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (j < k) top_weight[t * k + j] = bv[j] / total;
+    if (shifted != nullptr) {
+      for (int e = 0; e < num_experts; ++e) {
+        const float v = row[e];
+        const bool pick = (picked_bits[lane * words + (e >> 5)] >> (e & 31)) & 1u;
+        shifted[static_cast<int64_t>(e) * num_tokens + t] = pick ? v : v - 1.0f;
+      }
+    }
+  }
+  if (chunk_counts != nullptr) {
+    __syncthreads();
+    for (int e = lane; e < num_experts; e += 64)
+      chunk_counts[static_cast<int64_t>(blockIdx.x) * num_experts + e] = hist[e];
+  }
 }
 
 // Inclusive scan over the lanes of one 1024-lane workgroup.
@@ -577,6 +672,21 @@ int launch_topk(const float* scores, int64_t num_tokens, int32_t num_experts, in
                 int32_t* chunk_counts, int32_t* top_idx, float* top_weight, hipStream_t s) {
   const uint32_t groups = static_cast<uint32_t>((num_tokens + kTopkTokensPerGroup - 1) / kTopkTokensPerGroup);
   const int per = (num_experts + 63) / 64;
+  // A lane per token unless its insertion work (E x the rounded-up k) is
+  // large; SPARSEBENCH_TOPK_KERNEL=1 forces the wave form, 2 the lane form.
+  const int kmax = k <= 1 ? 1 : k <= 2 ? 2 : k <= 4 ? 4 : k <= 8 ? 8 : 16;
+  const int forced = tuning_override("SPARSEBENCH_TOPK_KERNEL");
+  if (forced == 2 || (forced != 1 && kmax * num_experts <= 2048)) {
+#define SB_TOPK_LANE(K) \
+  router_topk_lane_kernel<K><<<groups, 64, 0, s>>>(scores, num_tokens, num_experts, k, shifted, chunk_counts, top_idx, top_weight)
+    if (k <= 1) SB_TOPK_LANE(1);
+    else if (k <= 2) SB_TOPK_LANE(2);
+    else if (k <= 4) SB_TOPK_LANE(4);
+    else if (k <= 8) SB_TOPK_LANE(8);
+    else SB_TOPK_LANE(16);
+#undef SB_TOPK_LANE
+    return check_launch("router top-k");
+  }
 #define SB_TOPK(P)                                                                                          \
   router_topk_kernel<P><<<groups, kTopkThreads, 0, s>>>(scores, num_tokens, num_experts, k, shifted, chunk_counts, \
                                                         top_idx, top_weight)

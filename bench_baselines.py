@@ -3,7 +3,7 @@ computing it on the same MI355X (the measurements of the reference's
 bench/bench_moe.py and bench/bench_token_rounding.py, made here).
 
     python bench_baselines.py                 # both tables, markdown on stdout
-    python bench_baselines.py --only layer    # or: --only rounding, --only ceilings
+    python bench_baselines.py --only layer    # or: --only rounding, --only replay, --only ceilings
 
 Layer pipelines (everything from the routing to the [T, D] output is timed,
 host syncs included):
@@ -21,6 +21,13 @@ Token rounding (SonicMoE; the router's scores from workloads.router_scores):
   moe_forward_assigned and for the grouped_mm pipeline on the same list; the
   rounding step alone (routing.route_rounded: rounding, its list and its
   layout, no sync); and moe_forward_rounded (rounding fused into the layer).
+
+Replay sweep (D=2048, F=768, E=128, top-2, Zipf over a
+permutation): moe_forward captured once in a graph with buffers for
+T=16384, then replayed with fresh seeded x, routing and gates (seeds 1-4)
+at T' in {512, 2048, 8192, 16384}, the token count a device scalar read
+on the GPU each replay. Each replay is checked bit for bit against an eager
+moe_forward at T'.
 
 Ceilings (the box's practical roofs, next to the published 8 TB/s and
 2.5 PFLOP/s): streaming reads of 2 GiB with 16-byte vector loads and through
@@ -44,7 +51,7 @@ import torch.nn.functional as F
 from sparsebench_amd.moe import moe_forward, moe_forward_assigned, moe_forward_rounded
 from sparsebench_amd.routing import route_rounded
 from sparsebench_amd.token_rounding import token_rounding, top_k_assignments
-from sparsebench_amd.workloads import SHAPES, make_layer, router_scores
+from sparsebench_amd.workloads import SHAPES, make_layer, router_scores, routing_case, softmax_gates
 
 TOL = 3e-2
 FLUSH_BYTES = 512 << 20
@@ -202,6 +209,40 @@ def rounding_table(flush: torch.Tensor) -> list[str]:
     return lines
 
 
+def replay_table(flush: torch.Tensor) -> list[str]:
+    lines = ["| T' | seed | replay ms | useful TFLOP/s | eager at T' (ms) | bit-identical to eager |",
+             "|---:|---:|---:|---:|---:|---|"]
+    print("\n".join(lines), flush=True)
+    shape = SHAPES["replay_sweep"]
+    t_max = shape.num_tokens
+    x, idx, gates, w1, w2 = make_layer(shape, "zipf_perm", 0)
+    valid = torch.tensor([t_max], dtype=torch.int32, device="cuda")
+    run = lambda: moe_forward(x, idx, gates, w1, w2, valid_tokens=valid)  # noqa: E731
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+    flops_per_token = 2 * 2 * shape.top_k * shape.d_model * shape.ffn_dim
+    for seed, t in zip((1, 2, 3, 4), (512, 2048, 8192, 16384)):
+        g = torch.Generator(device="cuda").manual_seed(seed)  # fresh x, routing and gates, written in place
+        x.copy_(torch.randn(t_max, shape.d_model, generator=g, device="cuda"))
+        idx.copy_(routing_case("zipf_perm", t_max, shape.num_experts, seed, shape.top_k))
+        gates.copy_(softmax_gates(t_max, shape.top_k, seed + 1, "cuda"))
+        valid.fill_(t)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = lambda t=t: moe_forward(x[:t], idx[:t], gates[:t], w1, w2)  # noqa: E731
+        same = torch.equal(out[:t], eager())
+        ms = time_ms(graph.replay, flush)
+        ms_eager = time_ms(eager, flush)
+        lines.append(f"| {t} | {seed} | {ms:.3f} | {flops_per_token * t / ms / 1e9:.0f} | {ms_eager:.3f} | {same} |")
+        print(lines[-1], flush=True)
+    del x, idx, gates, w1, w2, out
+    torch.cuda.empty_cache()
+    return lines
+
+
 def ceilings_table(flush: torch.Tensor) -> list[str]:
     from sparsebench_amd import _C
 
@@ -234,7 +275,7 @@ def ceilings_table(flush: torch.Tensor) -> list[str]:
 
 def main() -> None:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("--only", choices=["layer", "rounding", "ceilings"])
+    p.add_argument("--only", choices=["layer", "rounding", "replay", "ceilings"])
     args = p.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit("bench_baselines.py needs a GPU")
@@ -247,6 +288,10 @@ def main() -> None:
     if args.only in (None, "rounding"):
         print("## Token rounding (tile 128, top-2)\n", flush=True)
         rounding_table(flush)
+        print(flush=True)
+    if args.only in (None, "replay"):
+        print("## Graph replay sweep (config 5: captured at T=16384)\n", flush=True)
+        replay_table(flush)
         print(flush=True)
     if args.only in (None, "ceilings"):
         print("## Ceilings of this box\n", flush=True)

@@ -147,3 +147,30 @@ def test_rejects_mismatched_shapes() -> None:
         moe_forward(x, idx, weight, w1, w2[:, :128])
     with pytest.raises(ValueError, match="x must be"):
         moe_forward(x, idx, weight[:, :1], w1, w2)
+
+
+def test_replay_sweep_config_is_bit_identical_to_eager() -> None:
+    # BASELINE config 5 at its real shape: captured once for T = 16384, then
+    # replayed with fresh x / routing / gates at fewer tokens; every replay
+    # equals an eager layer at that token count, bit for bit.
+    from sparsebench_amd.moe import moe_forward
+    from sparsebench_amd.workloads import SHAPES
+
+    shape = SHAPES["replay_sweep"]
+    t_max = shape.num_tokens
+    x, idx, gates, w1, w2 = make_layer(shape, "zipf_perm", 0)
+    valid = torch.tensor([t_max], dtype=torch.int32, device="cuda")
+    moe_forward(x, idx, gates, w1, w2, valid_tokens=valid)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = moe_forward(x, idx, gates, w1, w2, valid_tokens=valid)
+    for seed, t in zip((1, 2, 3, 4), (512, 2048, 8192, 16384)):
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        x.copy_(torch.randn(t_max, shape.d_model, generator=g, device="cuda"))
+        idx.copy_(routing_case("zipf_perm", t_max, shape.num_experts, seed, shape.top_k))
+        gates.copy_(softmax_gates(t_max, shape.top_k, seed + 1, "cuda"))
+        valid.fill_(t)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[:t], moe_forward(x[:t], idx[:t], gates[:t], w1, w2)), t

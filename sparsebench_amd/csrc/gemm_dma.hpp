@@ -520,13 +520,6 @@ struct DmaMainloop {
     __syncthreads();
   }
 
-  // 16-byte store with the non-temporal hint: the tile is written once and
-  // read back by the next kernel, so keeping it in L2 would only evict the
-  // operand rows other tiles still reuse (measured: -8% on SDD).
-  __device__ __forceinline__ static void store_streaming(void* p, u32x4_t v) {
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(p));
-  }
-
   // fn(r, col, chunk16): every 16-byte chunk of the staged tile, row by row
   // (col = first of its 8 columns), consecutive lanes on consecutive chunks.
   template <class Fn>

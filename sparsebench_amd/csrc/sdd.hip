@@ -200,7 +200,9 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   ML::run(lds, src, d_model / Cfg::BK, acc);
 
   // GELU, bf16, staged in LDS; then C[m, f] -> block begin + f/128, row m,
-  // column f % 128, whole 256-byte block rows per store instruction.
+  // column f % 128, whole 256-byte block rows per store instruction. Plain
+  // stores: DSD reads H right after, and a non-temporal hint here makes SDD
+  // alone faster but the layer slower (DSD then misses on H).
   if (apply_gelu)
     ML::stage_tile(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
   else
@@ -208,7 +210,7 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   uint16_t* blocks = out + static_cast<int64_t>(begin) * kBS * kBS;
   ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
     const int f = n0 + col;
-    ML::store_streaming(blocks + static_cast<int64_t>(f / kBS) * kBS * kBS + m * kBS + (f % kBS), v);
+    *reinterpret_cast<u32x4_t*>(blocks + static_cast<int64_t>(f / kBS) * kBS * kBS + m * kBS + (f % kBS)) = v;
   });
 }
 

@@ -93,6 +93,34 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
            int64_t nnz, int64_t w_rows, int64_t num_row_blocks, int64_t block_size, int64_t d_model,
            int32_t zero_dead_rows, void* stream);
 
+/* Replace the SDD and DSD stages of moe_forward (sparsebench/moe.py:46-48:
+ * spmm.sdd then spmm.dsd version 5 on route_device's layout). Each call
+ * enqueues one kernel whose workgroups choose, on the GPU and all alike from
+ * tokens_per_expert, between tiles that follow each expert's real rows and
+ * row-block tiles of sb_sdd's / sb_dsd's default shape. The expert tiles
+ * run when the routing is balanced (no expert holds
+ * more than twice the mean rows; for SDD also at most 256 rows per expert
+ * on average): an expert's weights are then streamed once per chunk of up
+ * to 160 rows (SDD) or 256 rows (DSD) instead of once per row block, and
+ * padding rows past the last 32-row group are neither computed nor read.
+ * The layout arrays are sb_routing's outputs (or those of
+ * sb_routing_assigned / sb_token_rounding); max_row_blocks is its
+ * worst-case row block count and num_copies the length of its copy_row.
+ * Every real row of out equals, bit for bit, what sb_sdd / sb_dsd write for
+ * it. sb_sdd_experts writes zeros on the padding rows up to each expert's
+ * next multiple of 32 rows; other padding rows may be left unwritten, as
+ * may every padding row of sb_dsd_experts's out[max_row_blocks*128, D].
+ * SDD: D % 64 == 0, F % 256 == 0. DSD: F % 128 == 0, D % 256 == 0, and h
+ * (max_row_blocks*F/128 blocks) under 2 GB. */
+int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+                   const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
+                   void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
+                   int64_t max_row_blocks, int32_t apply_gelu, void* stream);
+int sb_dsd_experts(const void* h, const void* w2, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
+                   const int32_t* row_block_expert, const int32_t* row_offsets, const int32_t* col_indices, void* out,
+                   int64_t max_row_blocks, int64_t num_experts, int64_t num_copies, int64_t ffn_dim, int64_t d_model,
+                   void* stream);
+
 /* Replaces the combine step of moe_forward (sparsebench/moe.py:51-54).
  * out[t, :] = bf16( sum_j fp32(y[copy_row[t*k+j], :]) * fp32(gates[t*k+j]) ),
  * j in [0, k), fp32 accumulation. Copies with copy_row < 0 add nothing.

@@ -251,6 +251,93 @@ def dsd_cuda(
     return out
 
 
+def _check_expert_layout(topo, device: torch.device) -> None:
+    if topo.block_size != 128:
+        _fail(f"expert tiles need block size 128, got {topo.block_size}")
+    for name in ("tokens_per_expert", "padded_offsets", "row_token", "row_block_expert", "row_offsets", "col_indices"):
+        t = getattr(topo, name)
+        _check_index(t, name)
+        if t.device != device:
+            _fail("all inputs must be on the same GPU")
+    if topo.padded_offsets.numel() != topo.num_experts + 1 or topo.tokens_per_expert.numel() != topo.num_experts:
+        _fail("tokens_per_expert / padded_offsets do not match the expert count")
+    max_row_blocks = topo.row_token.numel() // 128
+    if (topo.row_token.numel() != max_row_blocks * 128 or topo.row_block_expert.numel() != max_row_blocks
+            or topo.row_offsets.numel() != max_row_blocks + 1
+            or topo.col_indices.numel() != max_row_blocks * topo.ffn_blocks):
+        _fail("the routing layout's arrays do not have worst-case sizes of one layout")
+
+
+def sdd_experts_cuda(x: torch.Tensor, w1: torch.Tensor, topo, apply_gelu: bool) -> torch.Tensor:
+    """SDD of the MoE layer (this build's addition): expert-major tiles when
+    the routing is balanced, else the per-row-block kernel, chosen on the GPU.
+
+    topo: a routing layout from route_device / route_assigned / route_rounded.
+    Returns H blocks [max_row_blocks*F/128, 128, 128] bf16 whose real rows are
+    bit-identical to sdd_cuda's; padding rows past each expert's last 32-row
+    group may be left unwritten (the layer never reads them).
+    """
+    if not (x.is_cuda and w1.is_cuda and x.device == w1.device):
+        _fail("x and w1 must be on the same GPU")
+    if x.dtype != torch.bfloat16 or w1.dtype != torch.bfloat16:
+        _fail("x and w1 must be bfloat16")
+    if not (x.is_contiguous() and w1.is_contiguous()):
+        _fail("x and w1 must be contiguous")
+    if not (x.dim() == 2 and w1.dim() == 3 and w1.shape[1] == x.shape[1]):
+        _fail(f"x must be [T, D] and w1 [E, D, F], got {_shape(x)} and {_shape(w1)}")
+    _check_expert_layout(topo, x.device)
+    num_experts, d_model, ffn_dim = w1.shape
+    if num_experts != topo.num_experts or ffn_dim != topo.ffn_blocks * 128:
+        _fail("w1 does not match the routing layout")
+    max_row_blocks = topo.row_token.numel() // 128
+    out = torch.empty(max_row_blocks * (ffn_dim // 128), 128, 128, dtype=w1.dtype, device=w1.device)
+    check(lib().sb_sdd_experts(
+        x.data_ptr(), w1.data_ptr(), topo.row_token.data_ptr(), topo.row_block_expert.data_ptr(),
+        topo.row_offsets.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
+        out.data_ptr(), x.shape[0], d_model, ffn_dim, num_experts, max_row_blocks, 1 if apply_gelu else 0,
+        stream_of(x.device),
+    ))
+    return out
+
+
+def dsd_experts_cuda(h: torch.Tensor, w2_cat: torch.Tensor, topo) -> torch.Tensor:
+    """DSD (version 5) of the MoE layer (this build's addition): expert-major
+    tiles when the routing is balanced, else the per-row-block kernel, chosen
+    on the GPU.
+
+    h: sdd_experts_cuda's (or sdd_cuda's) blocks on topo's layout; w2_cat
+    [E*F, D]. Returns y [max_row_blocks*128, D] bf16 whose real rows are
+    bit-identical to dsd_cuda's; padding rows may be left unwritten.
+    """
+    if not (h.is_cuda and w2_cat.is_cuda and h.device == w2_cat.device):
+        _fail("h and w must be on the same GPU")
+    if h.dtype != torch.bfloat16 or w2_cat.dtype != torch.bfloat16:
+        _fail("h and w must be bfloat16")
+    if not (h.is_contiguous() and w2_cat.is_contiguous()):
+        _fail("h and w must be contiguous")
+    _check_expert_layout(topo, h.device)
+    max_row_blocks = topo.row_token.numel() // 128
+    ffn_dim = topo.ffn_blocks * 128
+    if h.dim() != 3 or h.shape != (max_row_blocks * topo.ffn_blocks, 128, 128):
+        _fail(f"h must be [{max_row_blocks * topo.ffn_blocks}, 128, 128] for this layout, got {_shape(h)}")
+    if w2_cat.dim() != 2 or w2_cat.shape[0] != topo.num_experts * ffn_dim:
+        _fail(f"w must be [E*F, D] = [{topo.num_experts * ffn_dim}, D], got {_shape(w2_cat)}")
+    d_model = w2_cat.shape[1]
+    out = torch.empty(max_row_blocks * 128, d_model, dtype=w2_cat.dtype, device=w2_cat.device)
+    check(lib().sb_dsd_experts(
+        h.data_ptr(), w2_cat.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
+        topo.row_block_expert.data_ptr(), topo.row_offsets.data_ptr(), topo.col_indices.data_ptr(), out.data_ptr(),
+        max_row_blocks, topo.num_experts, topo.copy_row.numel(), ffn_dim, d_model, stream_of(h.device),
+    ))
+    return out
+
+
+def expert_tiles_fit(d_model: int, ffn_dim: int, max_row_blocks: int) -> bool:
+    """Whether sdd_experts_cuda / dsd_experts_cuda take this shape (else the per-row-block kernels)."""
+    h_bytes = max_row_blocks * (ffn_dim // 128) * 128 * 128 * 2
+    return (d_model % 256 == 0 and ffn_dim % 256 == 0 and h_bytes < 2**31 and ffn_dim * d_model * 2 < 2**31)
+
+
 def combine_cuda(
     y: torch.Tensor,
     copy_row: torch.Tensor,

@@ -36,6 +36,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "sb_sdd": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]),
     "sb_dsd": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]),
+    "sb_sdd_experts": (
+        _c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]
+    ),
+    "sb_dsd_experts": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr]),
     "sb_read_probe": (_c_int, [_ptr, _i64, _i32, ctypes.c_uint32, _ptr, _ptr]),
     "sb_combine": (_c_int, [_ptr, _ptr, _ptr, _i32, _ptr, _i64, _i32, _i64, _i64, _ptr, _ptr]),
     "sb_routing_assigned": (

@@ -25,7 +25,7 @@ BUILD = ROOT / "_build"
 LIB_NAME = "libsparsebench_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ["probe.hip", "routing.hip", "sdd.hip", "dsd.hip", "combine.hip", "assigned.hip", "router.hip"]
+SOURCES = ["probe.hip", "routing.hip", "sdd.hip", "dsd.hip", "combine.hip", "assigned.hip", "router.hip", "experts.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

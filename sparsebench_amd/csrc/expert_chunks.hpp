@@ -1,0 +1,169 @@
+// The expert chunks of a routing layout, and the choice between the
+// expert-major and the per-row-block kernels of the MoE layer.
+//
+// The layout gives expert e n = tokens_per_expert[e] real rows from padded
+// row padded_offsets[e], in ceil(n / 128) row blocks, real rows first. A
+// chunk is a run of up to 32 RMAX of those rows that one tile computes:
+// chunks of S = 128 floor(32 RMAX / 128) rows, the last one holding what
+// remains, and a last piece of at most 32 RMAX - S rows joined to the chunk
+// before it. Every workgroup derives the chunks itself from
+// tokens_per_expert with wave scans, so no launch or buffer is added.
+#pragma once
+
+#include "common.hpp"
+
+namespace sb {
+
+constexpr int kBS = 128;
+
+// Chunks of an expert with n real rows, for tiles of at most 32 * RMAX rows.
+template <int RMAX>
+struct Chunking {
+  static_assert(RMAX >= 4 && RMAX <= 8, "a tile holds one to two row blocks");
+  static constexpr int kRows = kBS * ((32 * RMAX) / kBS);  // rows of a full chunk
+  static constexpr int kMerge = 32 * RMAX - kRows;         // a last piece up to this size joins the one before
+  __device__ __forceinline__ static int count(int32_t n) {
+    if (n <= 0) return 0;
+    const int c = (n + kRows - 1) / kRows;
+    const int last = n - kRows * (c - 1);
+    return c - ((c >= 2 && last <= kMerge) ? 1 : 0);
+  }
+};
+
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+
+struct Chunk {
+  int32_t expert;  // -1: no such chunk
+  int32_t row0;    // first padded row (a multiple of 128)
+  int32_t rows;    // real rows, 1 .. 32 * groups
+  int32_t groups;  // 32-row groups of the tile
+};
+
+// Chunk c (0 <= c < the number of chunks) in expert order.
+template <int RMAX>
+__device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_per_expert,
+                                            const int32_t* __restrict__ padded_offsets, int32_t num_experts, int c) {
+  const int lane = threadIdx.x & 63;
+  Chunk ch{-1, 0, 0, 0};
+  int before = 0;  // chunks of the experts before this pass
+  for (int base = 0; base < num_experts; base += 64) {
+    const int e = base + lane;
+    const int32_t n = e < num_experts ? tokens_per_expert[e] : 0;
+    const int cc = Chunking<RMAX>::count(n);
+    const int incl = wave_inclusive_scan(cc);
+    const uint64_t reach = __ballot(before + incl > c);  // experts whose chunks run past c
+    if (reach != 0) {
+      const int l = __builtin_ctzll(reach);  // the first of them holds chunk c
+      const int i = c - (before + __shfl(incl - cc, l, 64));
+      const int count = __shfl(cc, l, 64);
+      const int32_t n_e = __shfl(n, l, 64);
+      const int start = Chunking<RMAX>::kRows * i;
+      ch.expert = base + l;
+      ch.row0 = padded_offsets[base + l] + start;
+      ch.rows = i + 1 < count ? Chunking<RMAX>::kRows : n_e - start;
+      ch.groups = (ch.rows + 31) / 32;
+      break;
+    }
+    before += __shfl(incl, 63, 64);
+  }
+  ch.expert = __builtin_amdgcn_readfirstlane(ch.expert);
+  ch.row0 = __builtin_amdgcn_readfirstlane(ch.row0);
+  ch.rows = __builtin_amdgcn_readfirstlane(ch.rows);
+  ch.groups = __builtin_amdgcn_readfirstlane(ch.groups);
+  return ch;
+}
+
+// Which tiling computes a stage of the MoE layer: expert chunks or row
+// blocks. Every workgroup of the stage's kernel makes the same choice from
+// the same counts, so it costs no host sync.
+//   kGateDsd  expert tiles when the routing is balanced: no expert holds
+//             more than twice the mean rows. Skewed routing keeps row
+//             blocks: their tiles are all one size, and the many row blocks
+//             of a popular expert run side by side and share its weight
+//             lines in L2, where expert chunks of very different sizes
+//             leave CUs idle.
+//   kGateSdd  as kGateDsd, and at most 256 rows per expert on average: the
+//             case where merging an expert's last, nearly empty row block
+//             into a 160-row tile saves a whole stream of its weights. With
+//             many blocks per expert the row-block tiles are faster.
+enum ExpertGate : int32_t { kGateNone = 0, kGateDsd = 1, kGateSdd = 2 };
+
+// What a workgroup needs to choose and to number its tiles, from one pass
+// over tokens_per_expert (every wave computes the same values).
+struct LayoutSummary {
+  int64_t rows;      // real rows of all experts
+  int32_t largest;   // real rows of the largest expert
+  int32_t chunks_a;  // chunks of up to 32 RA rows
+  int32_t chunks_b;  // chunks of up to 32 RB rows
+};
+
+template <int RA, int RB>
+__device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restrict__ tokens_per_expert,
+                                                          int32_t num_experts) {
+  // All loads first (one per 64 experts, each behind a uniform branch), so
+  // they are in flight together: this runs before every tile's first DMA.
+  constexpr int kPasses = 1024 / 64;  // routing allows up to 1024 experts
+  const int lane = threadIdx.x & 63;
+  int32_t n[kPasses];
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    n[p] = 0;
+    if (64 * p < num_experts && 64 * p + lane < num_experts) n[p] = tokens_per_expert[64 * p + lane];
+  }
+  int64_t rows = 0;
+  int32_t most = 0, ca = 0, cb = 0;
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    if (64 * p >= num_experts) break;
+    const int32_t v = n[p] > 0 ? n[p] : 0;
+    rows += v;
+    most = max(most, v);
+    ca += Chunking<RA>::count(v);
+    cb += Chunking<RB>::count(v);
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    rows += __shfl_xor(rows, d, 64);
+    most = max(most, __shfl_xor(most, d, 64));
+    ca += __shfl_xor(ca, d, 64);
+    cb += __shfl_xor(cb, d, 64);
+  }
+  LayoutSummary sum;
+  sum.rows = rows;
+  sum.largest = __builtin_amdgcn_readfirstlane(most);
+  sum.chunks_a = __builtin_amdgcn_readfirstlane(ca);
+  sum.chunks_b = __builtin_amdgcn_readfirstlane(cb);
+  return sum;
+}
+
+__device__ __forceinline__ bool expert_tiles_chosen(const LayoutSummary& sum, int32_t num_experts, int32_t gate) {
+  const bool balanced = sum.rows > 0 && static_cast<int64_t>(sum.largest) * num_experts <= 2 * sum.rows;
+  const bool chosen = gate == kGateSdd ? balanced && sum.rows <= static_cast<int64_t>(256) * num_experts : balanced;
+  return __builtin_amdgcn_readfirstlane(chosen ? 1 : 0) != 0;
+}
+
+// Host side of the gate: SPARSEBENCH_EXPERT_GATE=1 forces the expert
+// tiles, 2 the row blocks (for tests and tuning); 0 or unset chooses.
+inline int32_t expert_gate_override() {
+  const int v = tuning_override("SPARSEBENCH_EXPERT_GATE");
+  return v == 1 || v == 2 ? v : 0;
+}
+
+// On the device: are the expert tiles of `gate`'s stage used?
+// force: 0 choose, 1 always, 2 never.
+__device__ __forceinline__ bool expert_stage_runs(const LayoutSummary& sum, int32_t num_experts, int32_t gate,
+                                                  int32_t force) {
+  if (force == 1) return true;
+  if (force == 2) return false;
+  return expert_tiles_chosen(sum, num_experts, gate);
+}
+
+}  // namespace sb

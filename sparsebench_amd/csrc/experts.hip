@@ -1,0 +1,449 @@
+// The SDD and DSD stages of the MoE layer, each one kernel that tiles either
+// by expert chunks or by row blocks, chosen on the device.
+//
+// The routing layout gives expert e n = tokens_per_expert[e] real rows,
+// stored from padded row padded_offsets[e] in ceil(n / 128) row blocks, real
+// rows first. The per-row-block kernels (sdd.hip, dsd.hip) stream all of an
+// expert's weight columns once per row block and compute the padding rows.
+// With near-uniform routing most experts hold a little more or less than
+// one block, so a second, nearly empty row block streams the whole weight
+// slice again (a third of SDD's HBM traffic at the fine-grained shape) and
+// about a quarter of the MFMAs run on padding.
+//
+// Expert tiles (expert_chunks.hpp): a tile covers one chunk of one expert's
+// rows, M = 32 R rows for the chunk's own R = ceil(rows / 32), with one row
+// of waves, each owning a column strip of all R 32-row groups, on the
+// LDS-DMA main loop (gemm_dma.hpp).
+//   SDD  chunks of up to 160 rows (RMAX 5: an expert with 129-160 rows is
+//        one tile), 512 columns per tile, 8 waves of 64 columns.
+//   DSD  chunks of up to 256 rows (RMAX 8), 256 columns per tile, 4 waves
+//        of 64 columns; at the fine-grained shape 64 experts x 4 slices is
+//        one tile per CU.
+// Rows of a chunk past its real rows are read as zeros (out-of-range DMA,
+// no memory read). SDD writes all 32 R rows of a chunk (padding rows as
+// GELU(0) = 0); DSD writes the real rows only. Padding rows past an
+// expert's last 32-row group are written by neither: nothing in the layer
+// reads them.
+//
+// Every workgroup computes the same choice from tokens_per_expert
+// (expert_tiles_chosen): expert tiles for balanced routing, else row-block
+// tiles with sb_sdd's / sb_dsd's default tile shape. Both live in one kernel
+// so the choice costs nothing: two launches, one of them returning at once,
+// cost about 10 us each (every workgroup holds up to 160 KB of LDS while it
+// reads the counts). The row-block tiles run on the expert tiles' own code
+// (sdd_chunk_tile / dsd_chunk_tile with the row block as a 128-row chunk,
+// every row read and written), which also needs fewer dependent loads
+// before the first DMA than the per-row-block kernels' tiles. Next to the
+// expert tiles in one kernel, dsd_row_block_tile's main loop gets a full
+// vmcnt(0) after every step's barrier from the compiler (its LDS-DMA alias
+// tracking loses the stages apart), which serialises its loads and MFMAs.
+
+#include "expert_chunks.hpp"
+#include "gelu.hpp"
+#include "gemm_dma.hpp"
+#include "layout.hpp"
+#include "sdd_tile.hpp"
+
+namespace sb {
+namespace {
+
+// Main-loop configuration of an R-group tile: M = 32 R, K steps of 32, one
+// row of WAVES waves, non-temporal weight loads, DMA issue spread over the
+// MFMAs (PIPE 3).
+template <int R, int BN, int WAVES, int STAGES>
+using ChunkCfg = DmaCfg<32 * R, BN, 32, STAGES, 1, WAVES, 0, 2, 3>;
+
+// LDS of the expert tiles of a kernel: the largest over its tile heights.
+template <int BN, int WAVES, int STAGES, int R>
+constexpr int chunk_lds_bytes() {
+  if constexpr (R == 1) {
+    return ChunkCfg<1, BN, WAVES, STAGES>::kLdsAlloc;
+  } else {
+    constexpr int a = ChunkCfg<R, BN, WAVES, STAGES>::kLdsAlloc;
+    constexpr int b = chunk_lds_bytes<BN, WAVES, STAGES, R - 1>();
+    return a > b ? a : b;
+  }
+}
+
+constexpr int max_int(int a, int b) { return a > b ? a : b; }
+
+// f(integral_constant<int, R>) for the chunk's R in 1 .. RMAX.
+template <int RMAX, class F>
+__device__ __forceinline__ void with_groups(int groups, F&& f) {
+  static_for<1, RMAX + 1>([&](auto rc) {
+    constexpr int R = decltype(rc)::value;
+    if (groups == R) f(rc);
+  });
+}
+
+// ------------------------------------------------------------------ SDD ---
+
+template <class Cfg>
+struct SddChunkSrc {
+  __amdgpu_buffer_rsrc_t x_rsrc, w_rsrc;
+  uint32_t a_off[Cfg::kAInstr];
+  uint32_t b_off[Cfg::kBInstr];
+  uint32_t b_step_bytes;
+  __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
+  __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
+  __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    *r = x_rsrc;
+    *s = static_cast<uint32_t>(t) * (Cfg::BK * 2);
+  }
+  __device__ __forceinline__ void b_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    *r = w_rsrc;
+    *s = static_cast<uint32_t>(t) * b_step_bytes;
+  }
+};
+
+struct SddArgs {
+  const uint16_t* x;
+  const uint16_t* w1;
+  const int32_t* row_token;
+  uint16_t* out;
+  int32_t num_tokens, d_model, ffn_dim;
+  int32_t apply_gelu;
+};
+
+template <class Cfg, bool kFastGelu>
+__device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const SddArgs& a, const Chunk& ch, int n0) {
+  using ML = DmaMainloop<Cfg>;
+  SddChunkSrc<Cfg> src;
+  src.x_rsrc = make_rsrc(a.x, static_cast<uint32_t>(a.num_tokens) * static_cast<uint32_t>(a.d_model) * 2u);
+  src.w_rsrc = make_rsrc(a.w1 + static_cast<int64_t>(ch.expert) * a.d_model * a.ffn_dim,
+                         static_cast<uint32_t>(a.d_model) * static_cast<uint32_t>(a.ffn_dim) * 2u);
+  src.b_step_bytes = static_cast<uint32_t>(Cfg::BK) * static_cast<uint32_t>(a.ffn_dim) * 2u;
+  const ADmaPos<Cfg> ap;
+#pragma unroll
+  for (int q = 0; q < Cfg::kAInstr; ++q) {
+    const int j = ap.row[q];  // row of the chunk; rows past BM belong to the rounded-up DMA area
+    const int32_t tok = j < ch.rows ? a.row_token[ch.row0 + j] : -1;
+    src.a_off[q] = (tok >= 0 && tok < a.num_tokens)
+                       ? static_cast<uint32_t>(tok) * static_cast<uint32_t>(a.d_model) * 2u + ap.chunk[q] * 16u
+                       : kOutOfRange;
+  }
+  const BDmaPos<Cfg> bp;
+#pragma unroll
+  for (int q = 0; q < Cfg::kBInstr; ++q)
+    src.b_off[q] = (static_cast<uint32_t>(bp.row[q]) * a.ffn_dim + n0 + bp.col[q]) * 2u;
+
+  typename ML::Acc acc;
+  ML::run(lds, src, a.d_model / Cfg::BK, acc);
+
+  if (a.apply_gelu)
+    ML::stage_tile(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
+  else
+    ML::stage_tile(lds, acc, [](float v) { return v; });
+  // Padded row p -> row block p / 128, whose blocks are (p / 128) * F/128 + f/128.
+  const int64_t ffn_blocks = a.ffn_dim / kBS;
+  ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
+    const int p = ch.row0 + m;
+    const int f = n0 + col;
+    *reinterpret_cast<u32x4_t*>(a.out + ((p / kBS) * ffn_blocks + f / kBS) * (kBS * kBS) + (p % kBS) * kBS +
+                                (f % kBS)) = v;
+  });
+}
+
+// Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 160 rows.
+constexpr int kSddBN = 512, kSddWaves = 8, kSddRmax = 5, kSddStages = 3;
+
+template <class CfgB, bool kFastGelu>
+__global__ void __launch_bounds__(64 * kSddWaves)
+    sdd_layer_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
+                     const int32_t* __restrict__ row_token, const int32_t* __restrict__ row_block_expert,
+                     const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ tokens_per_expert,
+                     const int32_t* __restrict__ padded_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
+                     int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t max_row_blocks,
+                     int32_t apply_gelu, int32_t group, int32_t force) {
+  static_assert(CfgB::kThreads == 64 * kSddWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
+  __shared__ __attribute__((aligned(1024)))
+  uint8_t lds[max_int(chunk_lds_bytes<kSddBN, kSddWaves, kSddStages, kSddRmax>(), CfgB::kLdsAlloc)];
+  const LayoutSummary sum = summarize_layout<kSddRmax, 4>(tokens_per_expert, num_experts);
+  const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
+  if (!expert_stage_runs(sum, num_experts, kGateSdd, force)) {
+    // Row blocks: the chunks of up to 128 rows are the live row blocks, in
+    // order; every row is computed and written (padding rows read as zeros).
+    const int blocks = sum.chunks_b;
+    const int slices = ffn_dim / CfgB::BN;
+    const int tile = xcd_remap(static_cast<int>(blockIdx.x), blocks * slices);
+    int rb, slice;
+    tile_coords(tile, blocks, slices, group, &rb, &slice);
+    if (rb >= blocks || rb >= max_row_blocks) return;
+    const int32_t expert = __builtin_amdgcn_readfirstlane(row_block_expert[rb]);
+    if (expert < 0 || expert >= num_experts) return;
+    sdd_chunk_tile<CfgB, kFastGelu>(lds, a, Chunk{expert, rb * kBS, kBS, 4}, slice * CfgB::BN);
+    return;
+  }
+  const int chunks = sum.chunks_a;
+  const int slices = ffn_dim / kSddBN;
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);
+  int c, slice;
+  tile_coords(tile, chunks, slices, group, &c, &slice);
+  if (c >= chunks) return;
+  const Chunk ch = find_chunk<kSddRmax>(tokens_per_expert, padded_offsets, num_experts, c);
+  // Not a routing layout (the chunk would leave the buffers): skip it.
+  if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kSddRmax ||
+      ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
+    return;
+  with_groups<kSddRmax>(ch.groups, [&](auto rc) {
+    constexpr int R = decltype(rc)::value;
+    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, kSddStages>, kFastGelu>(lds, a, ch, slice * kSddBN);
+  });
+}
+
+// ------------------------------------------------------------------ DSD ---
+
+// A: the chunk's rows of H, read in place. All of H is one buffer; lane row
+// j of the chunk sits in row block row0/128 + j/128 at row j % 128, so its
+// offset from the chunk's first block of the K step is fixed per lane, and
+// the step moves the scalar offset (4 steps of 32 per 128-wide block).
+template <class Cfg>
+struct DsdChunkSrc {
+  static constexpr int kStepsPerBlock = kBS / Cfg::BK;
+  __amdgpu_buffer_rsrc_t h_rsrc, w_rsrc;
+  uint32_t h_base;  // byte offset of the chunk's first H block
+  uint32_t w_step_bytes, n0_bytes;
+  uint32_t a_off[Cfg::kAInstr];
+  uint32_t b_off[Cfg::kBInstr];
+  __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
+  __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
+  __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    *r = h_rsrc;
+    *s = h_base + static_cast<uint32_t>(t / kStepsPerBlock) * (kBS * kBS * 2) +
+         static_cast<uint32_t>(t % kStepsPerBlock) * (Cfg::BK * 2);
+  }
+  __device__ __forceinline__ void b_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
+    *r = w_rsrc;
+    *s = static_cast<uint32_t>(t) * w_step_bytes + n0_bytes;
+  }
+};
+
+struct DsdArgs {
+  const uint16_t* h;
+  const uint16_t* w2;
+  uint16_t* out;
+  int64_t h_bytes;
+  int32_t ffn_dim, d_model;
+};
+
+template <class Cfg>
+__device__ __forceinline__ void dsd_chunk_tile(uint8_t* __restrict__ lds, const DsdArgs& a, const Chunk& ch, int n0) {
+  using ML = DmaMainloop<Cfg>;
+  const uint32_t ffn_blocks = static_cast<uint32_t>(a.ffn_dim / kBS);
+  DsdChunkSrc<Cfg> src;
+  src.h_rsrc = make_rsrc(a.h, static_cast<uint32_t>(a.h_bytes));
+  src.h_base = static_cast<uint32_t>(ch.row0 / kBS) * ffn_blocks * (kBS * kBS * 2);
+  src.w_rsrc = make_rsrc(a.w2 + static_cast<int64_t>(ch.expert) * a.ffn_dim * a.d_model,
+                         static_cast<uint32_t>(a.ffn_dim) * static_cast<uint32_t>(a.d_model) * 2u);
+  src.w_step_bytes = static_cast<uint32_t>(Cfg::BK) * static_cast<uint32_t>(a.d_model) * 2u;
+  src.n0_bytes = static_cast<uint32_t>(n0) * 2u;
+  const ADmaPos<Cfg> ap;
+#pragma unroll
+  for (int q = 0; q < Cfg::kAInstr; ++q) {
+    const uint32_t j = static_cast<uint32_t>(ap.row[q]);
+    src.a_off[q] = static_cast<int>(j) < ch.rows
+                       ? ((j / kBS) * ffn_blocks * (kBS * kBS) + (j % kBS) * kBS) * 2u + ap.chunk[q] * 16u
+                       : kOutOfRange;
+  }
+  const BDmaPos<Cfg> bp;
+#pragma unroll
+  for (int q = 0; q < Cfg::kBInstr; ++q)
+    src.b_off[q] = (static_cast<uint32_t>(bp.row[q]) * a.d_model + bp.col[q]) * 2u;
+
+  typename ML::Acc acc;
+  ML::run(lds, src, a.ffn_dim / Cfg::BK, acc);
+
+  ML::stage_tile(lds, acc, [](float v) { return v; });
+  uint16_t* out_tile = a.out + static_cast<int64_t>(ch.row0) * a.d_model + n0;
+  ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
+    if (m < ch.rows) *reinterpret_cast<u32x4_t*>(out_tile + static_cast<int64_t>(m) * a.d_model + col) = v;
+  });
+}
+
+// Expert tiles of the DSD: 4 waves, 256 columns, chunks of up to 256 rows.
+// Row-block tiles: 4 waves, 128 x CfgB::BN, every row of the row block read
+// and written, as sb_dsd's default tile does; they run on the same tile
+// code as the expert chunks (one H buffer, K steps through the row block's
+// own F/128 blocks, as the routing layout stores them).
+constexpr int kDsdBN = 256, kDsdWaves = 4, kDsdRmax = 8, kDsdStages = 4;
+
+template <class CfgB>
+__global__ void __launch_bounds__(64 * kDsdWaves)
+    dsd_layer_kernel(const uint16_t* __restrict__ h, const uint16_t* __restrict__ w2,
+                     const int32_t* __restrict__ tokens_per_expert, const int32_t* __restrict__ padded_offsets,
+                     const int32_t* __restrict__ row_block_expert, uint16_t* __restrict__ out, int64_t h_bytes,
+                     int32_t num_experts, int32_t ffn_dim, int32_t d_model, int32_t max_row_blocks, int32_t group,
+                     int32_t force) {
+  static_assert(CfgB::kThreads == 64 * kDsdWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
+  __shared__ __attribute__((aligned(1024)))
+  uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, kDsdWaves, kDsdStages, kDsdRmax>(), CfgB::kLdsAlloc)];
+  const LayoutSummary sum = summarize_layout<kDsdRmax, 4>(tokens_per_expert, num_experts);
+  const DsdArgs a{h, w2, out, h_bytes, ffn_dim, d_model};
+  if (!expert_stage_runs(sum, num_experts, kGateDsd, force)) {
+    // Row blocks: the chunks of up to 128 rows are the live row blocks, in order.
+    const int blocks = sum.chunks_b;
+    const int slices = d_model / CfgB::BN;
+    const int tile = xcd_remap(static_cast<int>(blockIdx.x), blocks * slices);
+    int rb, slice;
+    tile_coords(tile, blocks, slices, group, &rb, &slice);
+    if (rb >= blocks || rb >= max_row_blocks) return;
+    const int32_t expert = __builtin_amdgcn_readfirstlane(row_block_expert[rb]);
+    if (expert < 0 || expert >= num_experts) return;
+    const Chunk ch{expert, rb * kBS, kBS, 4};
+    dsd_chunk_tile<CfgB>(lds, a, ch, slice * CfgB::BN);
+    return;
+  }
+  const int chunks = sum.chunks_a;
+  const int slices = d_model / kDsdBN;
+  const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);
+  int c, slice;
+  tile_coords(tile, chunks, slices, group, &c, &slice);
+  if (c >= chunks) return;
+  const Chunk ch = find_chunk<kDsdRmax>(tokens_per_expert, padded_offsets, num_experts, c);
+  if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kDsdRmax ||
+      ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
+    return;
+  with_groups<kDsdRmax>(ch.groups, [&](auto rc) {
+    constexpr int R = decltype(rc)::value;
+    dsd_chunk_tile<ChunkCfg<R, kDsdBN, kDsdWaves, kDsdStages>>(lds, a, ch, slice * kDsdBN);
+  });
+}
+
+// --------------------------------------------------------------- launch ---
+
+template <class CfgB, bool kFastGelu>
+int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+                     const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
+                     void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
+                     int64_t max_row_blocks, int32_t apply_gelu, int32_t force, hipStream_t stream) {
+  // Both tilings have at most max_row_blocks x F/512 tiles (every chunk
+  // starts a row block of its own).
+  static_assert(CfgB::BN == kSddBN, "one grid for both tilings");
+  const int64_t tiles = max_row_blocks * (ffn_dim / kSddBN);
+  sdd_layer_kernel<CfgB, kFastGelu><<<static_cast<uint32_t>(tiles), 64 * kSddWaves, 0, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
+      tokens_per_expert, padded_offsets, static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens),
+      static_cast<int32_t>(d_model), static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts),
+      static_cast<int32_t>(max_row_blocks), apply_gelu, tile_group(), force);
+  return check_launch("sdd_experts");
+}
+
+template <bool kFastGelu>
+int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+                       const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
+                       void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
+                       int64_t max_row_blocks, int32_t apply_gelu, int32_t force, hipStream_t stream) {
+  // The row-block tile is sb_sdd's default for the shape (default_sdd_variant).
+  if (default_sdd_variant(d_model, ffn_dim) == 62)
+    return launch_sdd_layer<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 3>, kFastGelu>(
+        x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert, padded_offsets, out, num_tokens, d_model,
+        ffn_dim, num_experts, max_row_blocks, apply_gelu, force, stream);
+  return launch_sdd_layer<DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3>, kFastGelu>(
+      x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert, padded_offsets, out, num_tokens, d_model,
+      ffn_dim, num_experts, max_row_blocks, apply_gelu, force, stream);
+}
+
+template <class CfgB>
+int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
+                     const int32_t* row_block_expert, void* out, int64_t max_row_blocks, int64_t num_experts,
+                     int64_t num_copies, int64_t ffn_dim, int64_t d_model, int32_t force, hipStream_t stream) {
+  // Enough workgroups for either tiling, and few more: workgroups past the
+  // chosen tiling's tiles still read the counts before they return. Expert
+  // e's ceil(n_e / 256) chunks are at most 1 + (n_e - 1) / 256, so there
+  // are at most min(E, N) + N / 256 of them for N routed rows.
+  const int64_t rows = std::min(num_copies, max_row_blocks * kBS);
+  const int64_t chunk_bound = std::min(max_row_blocks, std::min(num_experts, rows) + rows / (32 * kDsdRmax));
+  const int64_t tiles = std::max(chunk_bound * (d_model / kDsdBN), max_row_blocks * (d_model / CfgB::BN));
+  const int64_t h_bytes = max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2;
+  dsd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kDsdWaves, 0, stream>>>(
+      static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w2), tokens_per_expert, padded_offsets,
+      row_block_expert, static_cast<uint16_t*>(out), h_bytes, static_cast<int32_t>(num_experts),
+      static_cast<int32_t>(ffn_dim), static_cast<int32_t>(d_model), static_cast<int32_t>(max_row_blocks),
+      tile_group(), force);
+  return check_launch("dsd_experts");
+}
+
+}  // namespace
+}  // namespace sb
+
+using namespace sb;
+
+extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_token,
+                              const int32_t* row_block_expert, const int32_t* row_offsets,
+                              const int32_t* tokens_per_expert, const int32_t* padded_offsets, void* out,
+                              int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
+                              int64_t max_row_blocks, int32_t apply_gelu, void* stream) {
+  constexpr int64_t kI32Max = 2147483647;
+  if (max_row_blocks < 0) return fail(SB_ERR_INVALID, "sdd_experts: negative row block count");
+  if (max_row_blocks == 0) return clear_ok();
+  if (!x || !w1 || !row_token || !row_block_expert || !row_offsets || !tokens_per_expert || !padded_offsets || !out)
+    return fail(SB_ERR_INVALID, "sdd_experts: null buffer");
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(out))
+    return fail(SB_ERR_INVALID, "x and w1 must be 16-byte aligned");
+  if (d_model <= 0 || d_model % 64 != 0)
+    return fail(SB_ERR_INVALID, "sdd needs D (%lld) to be a multiple of 64", static_cast<long long>(d_model));
+  if (ffn_dim <= 0 || ffn_dim % 256 != 0)
+    return fail(SB_ERR_INVALID, "sdd needs F (%lld) to be a multiple of 256", static_cast<long long>(ffn_dim));
+  if (num_tokens <= 0 || num_tokens > kI32Max || num_experts <= 0 || num_experts > kMaxExperts)
+    return fail(SB_ERR_INVALID, "sdd_experts: bad token or expert count");
+  if (num_tokens * d_model * 2 >= (int64_t{1} << 31) - 2 * d_model || ffn_dim * d_model * 2 >= (int64_t{1} << 31))
+    return fail(SB_ERR_INVALID, "sdd_experts: x or one expert's W1 too large for 32-bit buffer offsets");
+  if (max_row_blocks * kBS > kI32Max || max_row_blocks * (ffn_dim / kBS) > kI32Max)
+    return fail(SB_ERR_INVALID, "problem too large");
+  const int32_t force = expert_gate_override();
+  // The expert tiles are 512 wide; other widths take the per-row-block kernel.
+  if (ffn_dim % kSddBN != 0 || force == 2)
+    return sb_sdd(x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
+                  max_row_blocks, apply_gelu, stream);
+  const hipStream_t s = as_stream(stream);
+  const int rc = tuning_override("SPARSEBENCH_GELU_LIBM") > 0
+                     ? dispatch_sdd_layer<false>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
+                                                 padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
+                                                 max_row_blocks, apply_gelu, force, s)
+                     : dispatch_sdd_layer<true>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
+                                                padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
+                                                max_row_blocks, apply_gelu, force, s);
+  return rc ? rc : clear_ok();
+}
+
+extern "C" int sb_dsd_experts(const void* h, const void* w2, const int32_t* tokens_per_expert,
+                              const int32_t* padded_offsets, const int32_t* row_block_expert,
+                              const int32_t* row_offsets, const int32_t* col_indices, void* out,
+                              int64_t max_row_blocks, int64_t num_experts, int64_t num_copies, int64_t ffn_dim,
+                              int64_t d_model, void* stream) {
+  constexpr int64_t kI32Max = 2147483647;
+  if (max_row_blocks < 0) return fail(SB_ERR_INVALID, "dsd_experts: negative row block count");
+  if (max_row_blocks == 0) return clear_ok();
+  if (!h || !w2 || !tokens_per_expert || !padded_offsets || !row_block_expert || !row_offsets || !col_indices || !out)
+    return fail(SB_ERR_INVALID, "dsd_experts: null buffer");
+  if (!aligned16(h) || !aligned16(w2) || !aligned16(out)) return fail(SB_ERR_INVALID, "dsd_experts: unaligned buffer");
+  if (num_experts <= 0 || num_experts > kMaxExperts) return fail(SB_ERR_INVALID, "dsd_experts: bad expert count");
+  if (num_copies <= 0) return fail(SB_ERR_INVALID, "dsd_experts: bad copy count");
+  if (ffn_dim <= 0 || ffn_dim % kBS != 0)
+    return fail(SB_ERR_INVALID, "dsd_experts: F (%lld) must be a multiple of 128", static_cast<long long>(ffn_dim));
+  if (d_model <= 0 || d_model % kDsdBN != 0)
+    return fail(SB_ERR_INVALID, "dsd_experts: D (%lld) must be a multiple of 256", static_cast<long long>(d_model));
+  // H is read through one buffer and each expert's W2 through another, both
+  // with 32-bit offsets.
+  if (max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2 >= (int64_t{1} << 31) ||
+      ffn_dim * d_model * 2 >= (int64_t{1} << 31))
+    return fail(SB_ERR_INVALID, "dsd_experts: H or one expert's W2 too large for 32-bit buffer offsets");
+  if (max_row_blocks * kBS * d_model > (int64_t{1} << 62) || max_row_blocks * (d_model / kDsdBN) > kI32Max)
+    return fail(SB_ERR_INVALID, "problem too large");
+  const int32_t force = expert_gate_override();
+  // Row blocks forced: exactly sb_dsd version 5 (its default tile).
+  if (force == 2)
+    return sb_dsd(h, w2, row_offsets, col_indices, out, max_row_blocks * (ffn_dim / kBS), num_experts * ffn_dim,
+                  max_row_blocks, kBS, d_model, 0, stream);
+  const hipStream_t s = as_stream(stream);
+  // Row-block tile: sb_dsd's default 128 x 512 tile of 4 waves (v64);
+  // 128 x 256 when D % 512 != 0.
+  const int rc = d_model % 512 == 0
+                     ? launch_dsd_layer<ChunkCfg<4, 512, 4, 4>>(h, w2, tokens_per_expert, padded_offsets,
+                                                                row_block_expert, out, max_row_blocks, num_experts,
+                                                                num_copies, ffn_dim, d_model, force, s)
+                     : launch_dsd_layer<ChunkCfg<4, 256, 4, 4>>(h, w2, tokens_per_expert, padded_offsets,
+                                                                row_block_expert, out, max_row_blocks, num_experts,
+                                                                num_copies, ffn_dim, d_model, force, s);
+  return rc ? rc : clear_ok();
+}

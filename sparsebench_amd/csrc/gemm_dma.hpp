@@ -83,7 +83,12 @@ struct DmaCfg {
   static constexpr int TM = WTM / 32, TN = WTN / 32;
   static constexpr int kARowBytes = BK * 2;
   static constexpr int kAChunksPerRow = BK / 8;
-  static constexpr int kABytes = BM * kARowBytes;
+  // DMA instructions per wave per step for A, and the A area of a stage.
+  // When BM rows do not split into whole 1 KB rows per wave, the area is
+  // rounded up: the DMA rows past BM are loaded out of range (zeros, no
+  // memory read) and never read back.
+  static constexpr int kAInstr = (BM * kARowBytes + 1024 * kWaves - 1) / (1024 * kWaves);
+  static constexpr int kABytes = kAInstr * kWaves * 1024;
   static constexpr int kBRowBytes = BN * 2;
   static constexpr int kBBytes = BK * kBRowBytes;
   static constexpr int kStageBytes = kABytes + kBBytes;
@@ -91,7 +96,6 @@ struct DmaCfg {
   // LDS of a kernel: the ring, or the bf16 output tile staged through it in
   // the epilogue if that is larger.
   static constexpr int kLdsAlloc = kLdsBytes > BM * BN * 2 ? kLdsBytes : BM * BN * 2;
-  static constexpr int kAInstr = kABytes / 1024 / kWaves;  // DMA instructions per wave per step
   static constexpr int kBInstr = kBBytes / 1024 / kWaves;
   static constexpr int kLoadsPerStep = kAInstr + kBInstr;
   static constexpr int kARowsPerInstr = 1024 / kARowBytes;
@@ -101,7 +105,7 @@ struct DmaCfg {
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(BN == 128 || BN == 256 || BN == 512, "BN");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "waves own whole 32 x 32 blocks");
-  static_assert(kAInstr >= 1 && kAInstr * kWaves * 1024 == kABytes, "A step splits into whole 1 KB DMA rows");
+  static_assert(kAInstr >= 1 && kABytes >= BM * kARowBytes, "the A area holds BM rows");
   static_assert(kBInstr >= 1 && kBInstr * kWaves * 1024 == kBBytes, "B step splits into whole 1 KB DMA rows");
   static_assert(STAGES >= 2 && STAGES <= 8, "STAGES");
   static_assert(kLdsAlloc <= 160 * 1024, "LDS");

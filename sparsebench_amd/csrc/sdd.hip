@@ -16,33 +16,14 @@
 
 #include <type_traits>
 
+#include "expert_chunks.hpp"
+#include "gelu.hpp"
 #include "gemm_dma.hpp"
 #include "gemm_tile.hpp"
+#include "sdd_tile.hpp"
 
 namespace sb {
 namespace {
-
-constexpr int kBS = 128;
-
-// Exact-erf GELU, 0.5 v (1 + erf(v / sqrt 2)), in fp32.
-//
-// erfc(u) for u >= 0 by Abramowitz & Stegun 7.1.26 (Hastings' rational
-// approximation, |error| <= 1.5e-7): erfc(u) = t P(t) exp(-u^2),
-// t = 1 / (1 + p u). Branch-free, about fifteen instructions, and for
-// v < 0 it forms 1 - erf(u) = erfc(u) directly, with no cancellation.
-__device__ __forceinline__ float gelu_erf_fast(float v) {
-  const float u = fabsf(v) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, u, 1.0f));
-  float poly = fmaf(1.061405429f, t, -1.453152027f);
-  poly = fmaf(poly, t, 1.421413741f);
-  poly = fmaf(poly, t, -0.284496736f);
-  poly = fmaf(poly, t, 0.254829592f);
-  const float erfc_u = poly * t * __builtin_amdgcn_exp2f(-u * u * 1.44269504088896341f);
-  return v >= 0.0f ? v * (1.0f - 0.5f * erfc_u) : 0.5f * v * erfc_u;
-}
-
-// The same with the device library's erff (reference accuracy, slower).
-__device__ __forceinline__ float gelu_erf_libm(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f)); }
 
 template <class Cfg>
 struct SddLoader {
@@ -131,27 +112,6 @@ __global__ void __launch_bounds__(Cfg::kThreads)
   }
 }
 
-// The same tile on the LDS-DMA mainloop (gemm_dma.hpp): token rows are
-// gathered by the buffer loads themselves, padding rows read out of range
-// and land in LDS as zeros.
-template <class Cfg>
-struct SddDmaSrc {
-  __amdgpu_buffer_rsrc_t x_rsrc, w_rsrc;
-  uint32_t a_off[Cfg::kAInstr];
-  uint32_t b_off[Cfg::kBInstr];
-  uint32_t b_step_bytes;
-  __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
-  __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
-  __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
-    *r = x_rsrc;
-    *s = static_cast<uint32_t>(t) * (Cfg::BK * 2);
-  }
-  __device__ __forceinline__ void b_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
-    *r = w_rsrc;
-    *s = static_cast<uint32_t>(t) * b_step_bytes;
-  }
-};
-
 template <class Cfg, bool kFastGelu>
 __global__ void __launch_bounds__(Cfg::kThreads)
     sdd_dma_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
@@ -159,59 +119,10 @@ __global__ void __launch_bounds__(Cfg::kThreads)
                    const int32_t* __restrict__ row_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
                    int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t num_row_blocks, int32_t num_slices,
                    int32_t apply_gelu, int32_t group) {
-  using ML = DmaMainloop<Cfg>;
-  constexpr int BN = Cfg::BN;
-  static_assert(Cfg::BM == kBS, "one row block per tile");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::kLdsAlloc];
-
-  const int live_rb = live_row_blocks(row_offsets, num_row_blocks);
-  const int tile = xcd_remap(static_cast<int>(blockIdx.x), live_rb * num_slices);
-  int rb, slice;
-  tile_coords(tile, live_rb, num_slices, group, &rb, &slice);
-  const int n0 = slice * BN;
-  const int32_t begin = row_offsets[rb];
-  const int32_t end = row_offsets[rb + 1];
-  const int32_t ffn_blocks = ffn_dim / kBS;
-  if (begin == end) return;
-  const int32_t expert = row_block_expert[rb];
-  if (end - begin != ffn_blocks || begin < 0 || end > num_row_blocks * ffn_blocks || expert < 0 ||
-      expert >= num_experts)
-    return;
-
-  SddDmaSrc<Cfg> src;
-  src.x_rsrc = make_rsrc(x, static_cast<uint32_t>(num_tokens) * static_cast<uint32_t>(d_model) * 2u);
-  src.w_rsrc = make_rsrc(w1 + static_cast<int64_t>(expert) * d_model * ffn_dim,
-                         static_cast<uint32_t>(d_model) * static_cast<uint32_t>(ffn_dim) * 2u);
-  src.b_step_bytes = static_cast<uint32_t>(Cfg::BK) * static_cast<uint32_t>(ffn_dim) * 2u;
-  const ADmaPos<Cfg> ap;
-#pragma unroll
-  for (int q = 0; q < Cfg::kAInstr; ++q) {
-    const int32_t tok = row_token[static_cast<int64_t>(rb) * kBS + ap.row[q]];
-    src.a_off[q] = (tok >= 0 && tok < num_tokens)
-                        ? static_cast<uint32_t>(tok) * static_cast<uint32_t>(d_model) * 2u + ap.chunk[q] * 16u
-                        : kOutOfRange;
-  }
-  const BDmaPos<Cfg> bp;
-#pragma unroll
-  for (int q = 0; q < Cfg::kBInstr; ++q)
-    src.b_off[q] = (static_cast<uint32_t>(bp.row[q]) * ffn_dim + n0 + bp.col[q]) * 2u;
-
-  typename ML::Acc acc;
-  ML::run(lds, src, d_model / Cfg::BK, acc);
-
-  // GELU, bf16, staged in LDS; then C[m, f] -> block begin + f/128, row m,
-  // column f % 128, whole 256-byte block rows per store instruction. Plain
-  // stores: DSD reads H right after, and a non-temporal hint here makes SDD
-  // alone faster but the layer slower (DSD then misses on H).
-  if (apply_gelu)
-    ML::stage_tile(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
-  else
-    ML::stage_tile(lds, acc, [](float v) { return v; });
-  uint16_t* blocks = out + static_cast<int64_t>(begin) * kBS * kBS;
-  ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
-    const int f = n0 + col;
-    *reinterpret_cast<u32x4_t*>(blocks + static_cast<int64_t>(f / kBS) * kBS * kBS + m * kBS + (f % kBS)) = v;
-  });
+  sdd_row_block_tile<Cfg, kFastGelu>(lds, static_cast<int>(blockIdx.x), x, w1, row_token, row_block_expert,
+                                     row_offsets, out, num_tokens, d_model, ffn_dim, num_experts, num_row_blocks,
+                                     num_slices, apply_gelu, group);
 }
 
 // Persistent form (DmaMainloop::run_tiles): gridDim.x workgroups, about one
@@ -531,15 +442,12 @@ extern "C" int sb_sdd(const void* x, const void* w1, const int32_t* row_token, c
   const hipStream_t s = as_stream(stream);
   const int forced = tuning_override("SPARSEBENCH_SDD_VARIANT");
   const int gelu_mode = tuning_override("SPARSEBENCH_GELU_LIBM");
-  // Default, from timing every variant on the benchmark shapes (MI355X,
-  // samples interleaved across variants): 128 x 512 tiles of 8 waves, each
-  // 64 x 128 (8 MFMAs per 16-deep sub-step: enough work to cover the LDS
-  // fragment reads, 2 waves per SIMD), non-temporal weight loads, BK 32,
-  // the next stage's DMA and the next sub-step's fragment reads issued
-  // among the MFMAs; a 3-stage ring, or with a deep reduction (D >= 4096) a
-  // 4-stage one. F must be a multiple of 512; otherwise 128 x 256 tiles of
-  // 8 waves, BK 64 x 3 stages.
-  int variant = forced > 0 ? forced : (d_model >= 4096 ? 62 : 65);
+  // Default (default_sdd_variant): 128 x 512 tiles of 8 waves, each 64 x
+  // 128 (8 MFMAs per 16-deep sub-step: enough work to cover the LDS
+  // fragment reads, 2 waves per SIMD), non-temporal weight loads, the next
+  // stage's DMA and the next sub-step's fragment reads issued among the
+  // MFMAs.
+  int variant = forced > 0 ? forced : default_sdd_variant(d_model, ffn_dim);
   if (ffn_dim % 512 != 0 && ((variant >= 31 && variant <= 33) || variant == 52 || (variant >= 55 && variant <= 59)))
     variant = 25;
   if (ffn_dim % 512 != 0 && (variant == 61 || variant == 62 || variant == 64 || variant == 65)) variant = 63;

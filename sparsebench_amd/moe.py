@@ -10,6 +10,7 @@ real size from padded_offsets / row_offsets on the GPU.
 
 from __future__ import annotations
 
+import os
 from collections.abc import Callable
 
 import torch
@@ -23,6 +24,34 @@ STAGES = ("routing", "SDD + GELU (fused)", "DSD", "combine")
 
 def _no_mark(stage: str) -> None:
     pass
+
+
+def _expert_tiles(topo, d_model: int, ffn_dim: int) -> bool:
+    """SDD / DSD on expert-major tiles (the default), unless
+    SPARSEBENCH_EXPERT_TILES=0 or the shape needs the per-row-block kernels."""
+    from sparsebench_amd import _C
+
+    if os.environ.get("SPARSEBENCH_EXPERT_TILES", "1") == "0":
+        return False
+    return _C.expert_tiles_fit(d_model, ffn_dim, topo.row_token.numel() // topo.block_size)
+
+
+def _sdd_dsd(x, w1, w2, topo, mark):
+    """H = gelu(x grouped @ w1), then y = H @ w2 on topo's rows; marks both stages."""
+    from sparsebench_amd import _C
+
+    num_experts, d_model, ffn_dim = w1.shape
+    w2_cat = w2.view(num_experts * ffn_dim, d_model)
+    if _expert_tiles(topo, d_model, ffn_dim):
+        h = _C.sdd_experts_cuda(x, w1, topo, True)
+        mark("SDD + GELU (fused)")
+        y = _C.dsd_experts_cuda(h, w2_cat, topo)
+    else:
+        h = sdd(x, w1, topo, gelu=True)
+        mark("SDD + GELU (fused)")
+        y = dsd(h, w2_cat, topo, version=5)
+    mark("DSD")
+    return h, y
 
 
 def combine(
@@ -64,9 +93,9 @@ def moe_forward(
 
     topo = route_device(expert_idx, num_experts, ffn_dim, BLOCK_SIZE, valid_tokens)
     mark("routing")
-    h = sdd(x, w1, topo, gelu=True)
-    mark("SDD + GELU (fused)")
     if fused_combine and d_model % 256 == 0:
+        h = sdd(x, w1, topo, gelu=True)
+        mark("SDD + GELU (fused)")
         from sparsebench_amd import _C
 
         out = _C.dsd_combine_cuda(h, w2.view(num_experts * ffn_dim, d_model), topo.row_offsets, topo.col_indices,
@@ -74,8 +103,7 @@ def moe_forward(
         mark("DSD")
         mark("combine")
         return out
-    y = dsd(h, w2.view(num_experts * ffn_dim, d_model), topo, version=5)
-    mark("DSD")
+    _, y = _sdd_dsd(x, w1, w2, topo, mark)
     out = combine(y, topo.copy_row, expert_weight, valid_tokens)
     mark("combine")
     return out
@@ -84,12 +112,8 @@ def moe_forward(
 def _assigned_layer(x, routing: AssignedRouting, weight_of_copy, w1, w2, mark, valid_tokens) -> torch.Tensor:
     from sparsebench_amd import _C
 
-    num_experts, d_model, ffn_dim = w1.shape
     mark("routing")
-    h = sdd(x, w1, routing.topology, gelu=True)
-    mark("SDD + GELU (fused)")
-    y = dsd(h, w2.view(num_experts * ffn_dim, d_model), routing.topology, version=5)
-    mark("DSD")
+    _, y = _sdd_dsd(x, w1, w2, routing.topology, mark)
     out = _C.combine_assigned_cuda(y, routing.topology.copy_row, weight_of_copy, routing.token_offsets,
                                    routing.token_copies, x.shape[0], valid_tokens)
     mark("combine")

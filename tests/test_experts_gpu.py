@@ -1,0 +1,275 @@
+"""The SDD / DSD stages of moe_forward (sb_sdd_experts, sb_dsd_experts)
+against the per-row-block kernels and the oracle.
+
+Each entry point launches an expert-major kernel and the per-row-block
+kernel; on the GPU one of them does the work (the expert tiles when the
+routing is balanced). SPARSEBENCH_EXPERT_GATE=1 / 2 forces one side, so
+both are tested on every routing here, and 0 (unset) tests the choice.
+
+Every real row of H and of y must equal, bit for bit, what sdd_cuda /
+dsd_cuda write for it: both accumulate each output in fp32 over K in the same
+order of 16-deep MFMA steps, and a row's result depends on that row alone.
+SDD's padding rows up to the chunk's next multiple of 32 are zeros. The
+per-row-block kernels are themselves pinned to the oracle (test_sdd_gpu.py,
+test_dsd_gpu.py); one oracle check per variant is repeated here.
+
+The routings put experts on every side of the chunking's edges: 0, 1, 31,
+32, 33, 127, 128, 129, 160 (one 160-row tile), 161 (two tiles), 192, 255,
+256, 257 (a 256-row tile plus one more) and several blocks; more than 64
+experts make the in-kernel chunk search take several passes.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.moe_ref import dsd_rows, sdd_blocks
+from oracle.topology_ref import build_layout
+from sparsebench_amd.workloads import routing_case
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"rtol": 1.6e-2, "atol": 1.6e-2}
+GATES = ["0", "1", "2"]  # choose on the device / expert tiles / row blocks
+SDD_RMAX = 5  # the SDD expert tiles hold up to 160 rows
+EDGE_COUNTS = [0, 1, 31, 32, 33, 127, 128, 129, 160, 161, 192, 255, 256, 257, 300, 600, 0, 5]
+
+
+def edge_routing(seed: int) -> torch.Tensor:
+    """k = 1 routing giving expert e exactly EDGE_COUNTS[e] copies, in shuffled token order."""
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.repeat_interleave(torch.arange(len(EDGE_COUNTS)), torch.tensor(EDGE_COUNTS))
+    return idx[torch.randperm(idx.numel(), generator=g)].reshape(-1, 1).contiguous()
+
+
+CASES = {
+    # name: (expert_idx builder, E, D, F)
+    "edges": (lambda s: edge_routing(s), len(EDGE_COUNTS), 512, 512),
+    "uniform64": (lambda s: routing_case("random", 4096, 64, seed=s), 64, 512, 512),
+    "zipf130": (lambda s: routing_case("zipf_perm", 3000, 130, seed=s), 130, 512, 768),
+    "skewed": (lambda s: routing_case("skewed", 900, 8, seed=s), 8, 512, 256),
+    "one_expert": (lambda s: torch.zeros(200, 1, dtype=torch.int64), 1, 256, 512),
+    # The fine-grained shape's routing (every expert <= 160 rows with this
+    # seed) and F: 64 x 8 expert SDD tiles, 2 rounds on 256 CUs.
+    "uniform_wide": (lambda s: routing_case("random", 4096, 64, seed=1), 64, 256, 4096),
+}
+
+
+def real_rows(topo) -> np.ndarray:
+    """Padded row indices that hold a copy, from the device layout."""
+    cnt = topo.tokens_per_expert.cpu().numpy()
+    off = topo.padded_offsets.cpu().numpy()
+    return np.concatenate([np.arange(off[e], off[e] + cnt[e]) for e in range(len(cnt))]).astype(np.int64)
+
+
+def chunk_pad_rows(topo, rmax: int) -> np.ndarray:
+    """Padding rows that the expert kernels write (zeros): up to each last chunk's next multiple of 32."""
+    rows_full = 128 * ((32 * rmax) // 128)
+    merge = 32 * rmax - rows_full
+    out = []
+    for e, (n, o) in enumerate(zip(topo.tokens_per_expert.cpu().tolist(), topo.padded_offsets.cpu().tolist())):
+        if n <= 0:
+            continue
+        c = -(-n // rows_full)
+        if c >= 2 and n - rows_full * (c - 1) <= merge:
+            c -= 1
+        start = rows_full * (c - 1)
+        end = start + 32 * (-(-(n - start) // 32))
+        out.extend(range(o + n, o + end))
+    return np.asarray(out, dtype=np.int64)
+
+
+def dense_rows(blocks: torch.Tensor, ffn_blocks: int) -> torch.Tensor:
+    """H blocks [R*fb, 128, 128] -> dense [R*128, fb*128] (row p = padded row p)."""
+    rb = blocks.shape[0] // ffn_blocks
+    return blocks.view(rb, ffn_blocks, 128, 128).permute(0, 2, 1, 3).reshape(rb * 128, ffn_blocks * 128)
+
+
+def inputs(case: str, seed: int):
+    build, e, d, f = CASES[case]
+    g = torch.Generator().manual_seed(100 + seed)
+    idx = build(seed)
+    t = idx.shape[0]
+    x = torch.randn(t, d, generator=g).bfloat16()
+    w1 = (torch.randn(e, d, f, generator=g) / d**0.5).bfloat16()
+    w2 = (torch.randn(e, f, d, generator=g) / f**0.5).bfloat16()
+    return idx, x, w1, w2
+
+
+@pytest.mark.parametrize("gate", GATES)
+@pytest.mark.parametrize("case", list(CASES))
+def test_sdd_experts_rows_equal_row_block_kernel(monkeypatch, gate: str, case: str) -> None:
+    from sparsebench_amd import _C
+    from sparsebench_amd.routing import route_device
+    from sparsebench_amd.spmm import sdd
+
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    idx, x, w1, _ = inputs(case, int(gate))
+    e, _, f = w1.shape
+    topo = route_device(idx.cuda(), e, f, 128)
+    xc, w1c = x.cuda(), w1.cuda()
+    h_rb = dense_rows(sdd(xc, w1c, topo), f // 128)
+    h_ex = dense_rows(_C.sdd_experts_cuda(xc, w1c, topo, True), f // 128)
+    rows = torch.as_tensor(real_rows(topo), device="cuda")
+    assert torch.equal(h_ex[rows], h_rb[rows])
+    pad = torch.as_tensor(chunk_pad_rows(topo, SDD_RMAX), device="cuda")
+    if pad.numel():
+        assert torch.all(h_ex[pad] == 0)
+    if case == "edges":  # and against the oracle directly
+        lay = build_layout(idx.numpy(), e, f, 128)
+        ref = dense_rows(sdd_blocks(x.float(), w1.float(), lay), f // 128)
+        live = rows[rows < ref.shape[0]].cpu()
+        torch.testing.assert_close(h_ex[live.cuda()].float().cpu(), ref[live], **TOL)
+
+
+@pytest.mark.parametrize("gate", GATES)
+@pytest.mark.parametrize("case", list(CASES))
+def test_dsd_experts_rows_equal_row_block_kernel(monkeypatch, case: str, gate: str) -> None:
+    from sparsebench_amd import _C
+    from sparsebench_amd.routing import route_device
+    from sparsebench_amd.spmm import dsd, sdd
+
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    idx, x, w1, w2 = inputs(case, 10 + int(gate))
+    e, d, f = w1.shape
+    topo = route_device(idx.cuda(), e, f, 128)
+    h = sdd(x.cuda(), w1.cuda(), topo)
+    w2_cat = w2.cuda().view(e * f, d)
+    y_rb = dsd(h, w2_cat, topo, version=5)
+    y_ex = _C.dsd_experts_cuda(h, w2_cat, topo)
+    rows = torch.as_tensor(real_rows(topo), device="cuda")
+    assert torch.equal(y_ex[rows], y_rb[rows])
+    if case == "edges":
+        lay = build_layout(idx.numpy(), e, f, 128)
+        ref = dsd_rows(h[: lay.col_indices.size].float().cpu(), w2_cat.float().cpu(), lay)
+        live = rows[rows < ref.shape[0]].cpu()
+        torch.testing.assert_close(y_ex[live.cuda()].float().cpu(), ref[live], **TOL)
+
+
+@pytest.mark.parametrize("gate", GATES)
+def test_dsd_experts_padding_rows_do_not_reach_real_rows(monkeypatch, gate: str) -> None:
+    # Padding rows of H may hold anything (the expert SDD leaves some
+    # unwritten): the expert tiling does not read them, the row-block one
+    # reads them into padding rows of y only, which it does not write.
+    from sparsebench_amd import _C
+    from sparsebench_amd.routing import route_device
+    from sparsebench_amd.spmm import sdd
+
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    idx, x, w1, w2 = inputs("edges", 3)
+    e, d, f = w1.shape
+    topo = route_device(idx.cuda(), e, f, 128)
+    h = sdd(x.cuda(), w1.cuda(), topo)
+    w2_cat = w2.cuda().view(e * f, d)
+    clean = _C.dsd_experts_cuda(h, w2_cat, topo)
+    rows = torch.as_tensor(real_rows(topo), device="cuda")
+    fb = f // 128
+    pad_mask = torch.ones(h.shape[0] // fb * 128, dtype=torch.bool, device="cuda")
+    pad_mask[rows] = False
+    pad = pad_mask.nonzero().squeeze(1)
+    h.view(-1, fb, 128, 128)[pad // 128, :, pad % 128, :] = float("nan")  # in place, in h's own storage
+    assert torch.isnan(dense_rows(h, fb)[pad]).all()
+    dirty = _C.dsd_experts_cuda(h, w2_cat, topo)
+    assert torch.equal(dirty[rows], clean[rows])
+
+
+@pytest.mark.parametrize("gate", GATES)
+@pytest.mark.parametrize("case", ["uniform64", "zipf130", "edges", "skewed"])
+def test_moe_forward_expert_tiles_bit_identical(monkeypatch, case: str, gate: str) -> None:
+    from sparsebench_amd.moe import moe_forward
+
+    idx, x, w1, w2 = inputs(case, 21)
+    g = torch.Generator().manual_seed(5)
+    gates = torch.softmax(torch.randn(idx.shape, generator=g), dim=-1).bfloat16().cuda()
+    args = (x.cuda(), idx.cuda(), gates, w1.cuda(), w2.cuda())
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    ref = moe_forward(*args)
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    assert torch.equal(moe_forward(*args), ref)
+
+
+@pytest.mark.parametrize("gate", GATES)
+def test_moe_forward_rounded_expert_tiles_bit_identical(monkeypatch, gate: str) -> None:
+    from sparsebench_amd.moe import moe_forward_rounded
+    from sparsebench_amd.workloads import router_scores
+
+    t, e, d, f = 1500, 16, 256, 512
+    g = torch.Generator().manual_seed(9)
+    scores = router_scores("zipf", t, e, seed=2).cuda()
+    x = torch.randn(t, d, generator=g).bfloat16().cuda()
+    w1 = (torch.randn(e, d, f, generator=g) / math.sqrt(d)).bfloat16().cuda()
+    w2 = (torch.randn(e, f, d, generator=g) / math.sqrt(f)).bfloat16().cuda()
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    ref = moe_forward_rounded(x, scores, 2, w1, w2)
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    assert torch.equal(moe_forward_rounded(x, scores, 2, w1, w2), ref)
+
+
+def test_expert_kernels_reject_bad_shapes() -> None:
+    from sparsebench_amd import _C
+    from sparsebench_amd.routing import route_device
+
+    idx, x, w1, w2 = inputs("skewed", 0)
+    e, d, f = w1.shape
+    topo = route_device(idx.cuda(), e, f, 128)
+    with pytest.raises(RuntimeError, match="w1 does not match"):
+        _C.sdd_experts_cuda(x.cuda(), w1[:, :, :128].contiguous().cuda(), topo, True)
+    with pytest.raises(RuntimeError, match=r"h must be \["):
+        _C.dsd_experts_cuda(torch.zeros(3, 128, 128, dtype=torch.bfloat16, device="cuda"),
+                            w2.cuda().view(e * f, d), topo)
+
+
+def gate_rule(counts: list[int], stage: str) -> bool:
+    """The choice stated in expert_chunks.hpp, restated: expert tiles iff no
+    expert holds more than twice the mean rows (and, for SDD, the mean is at
+    most 256 rows)."""
+    counts = [max(c, 0) for c in counts]
+    total, most, e = sum(counts), max(counts), len(counts)
+    balanced = total > 0 and most * e <= 2 * total
+    return balanced and (stage == "dsd" or total <= 256 * e)
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_device_choice_follows_the_rule(case: str) -> None:
+    # The two paths leave different marks in a NaN-filled output: the
+    # row-block kernels write every row of every live row block, the expert
+    # tiles leave padding rows past an expert's last 32-row group (SDD) or
+    # every padding row (DSD) untouched.
+    from sparsebench_amd._lib import check, lib, stream_of
+    from sparsebench_amd.routing import route_device
+
+    idx, x, w1, w2 = inputs(case, 4)
+    e, d, f = w1.shape
+    topo = route_device(idx.cuda(), e, f, 128)
+    counts = topo.tokens_per_expert.cpu().tolist()
+    max_rb = topo.row_token.numel() // 128
+    fb = f // 128
+    xc, w1c, w2c = x.cuda(), w1.cuda(), w2.cuda().view(e * f, d)
+    h = torch.full((max_rb * fb, 128, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    check(lib().sb_sdd_experts(
+        xc.data_ptr(), w1c.data_ptr(), topo.row_token.data_ptr(), topo.row_block_expert.data_ptr(),
+        topo.row_offsets.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
+        h.data_ptr(), xc.shape[0], d, f, e, max_rb, 1, stream_of(xc.device)))
+    y = torch.full((max_rb * 128, d), float("nan"), dtype=torch.bfloat16, device="cuda")
+    check(lib().sb_dsd_experts(
+        h.data_ptr(), w2c.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
+        topo.row_block_expert.data_ptr(), topo.row_offsets.data_ptr(), topo.col_indices.data_ptr(), y.data_ptr(),
+        max_rb, e, topo.copy_row.numel(), f, d,
+        stream_of(xc.device)))
+    torch.cuda.synchronize()
+    off = topo.padded_offsets.cpu().tolist()
+    # Padding rows inside live row blocks, past each expert's last 32-row group.
+    untouched = [r for ex, n in enumerate(counts) if n > 0
+                 for r in range(off[ex] + 32 * (-(-n // 32)), off[ex + 1])]
+    pad = [r for ex, n in enumerate(counts) for r in range(off[ex] + n, off[ex + 1])]
+    dense = dense_rows(h, fb)
+    if f % 512 == 0 and untouched:
+        sdd_expert = bool(torch.isnan(dense[torch.tensor(untouched, device="cuda")]).all())
+        assert sdd_expert == gate_rule(counts, "sdd")
+    if pad:
+        dsd_expert = bool(torch.isnan(y[torch.tensor(pad, device="cuda")]).all())
+        assert dsd_expert == gate_rule(counts, "dsd")

@@ -98,11 +98,11 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
  * enqueues one kernel whose workgroups choose, on the GPU and all alike from
  * tokens_per_expert, between tiles that follow each expert's real rows and
  * row-block tiles of sb_sdd's / sb_dsd's default shape. The expert tiles
- * run when the routing is balanced (no expert holds
- * more than twice the mean rows; for SDD also at most 256 rows per expert
- * on average): an expert's weights are then streamed once per chunk of up
- * to 160 rows (SDD) or 256 rows (DSD) instead of once per row block, and
- * padding rows past the last 32-row group are neither computed nor read.
+ * run when no expert holds more than twice the mean rows, and for SDD also
+ * the experts hold at most 256 rows on average: an expert's weights
+ * are then streamed once per chunk of up to 192 rows (SDD) or 256 rows
+ * (DSD) instead of once per row block, and padding rows past the last
+ * 32-row group are neither computed nor read.
  * The layout arrays are sb_routing's outputs (or those of
  * sb_routing_assigned / sb_token_rounding); max_row_blocks is its
  * worst-case row block count and num_copies the length of its copy_row.

@@ -87,13 +87,18 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
 //   kGateDsd  expert tiles when the routing is balanced: no expert holds
 //             more than twice the mean rows. Skewed routing keeps row
 //             blocks: their tiles are all one size, and the many row blocks
-//             of a popular expert run side by side and share its weight
-//             lines in L2, where expert chunks of very different sizes
-//             leave CUs idle.
+//             of a popular expert run side by side and share its W2 lines
+//             in L2, where chunks of very different sizes leave CUs idle.
 //   kGateSdd  as kGateDsd, and at most 256 rows per expert on average: the
 //             case where merging an expert's last, nearly empty row block
-//             into a 160-row tile saves a whole stream of its weights. With
-//             many blocks per expert the row-block tiles are faster.
+//             into one tile saves a whole stream of its W1 slice (with many
+//             blocks per expert the row-block tiles are faster). The SDD's
+//             expert tiles leave padding rows past each expert's last
+//             32-row group unwritten, so they must only feed the DSD's
+//             expert tiles, which do not read them: kGateSdd implies
+//             kGateDsd. (A row-block DSD would read those rows, cold from
+//             HBM rather than from the cache the SDD's stores warm: with
+//             skewed routing that costs it more than the SDD gains.)
 enum ExpertGate : int32_t { kGateNone = 0, kGateDsd = 1, kGateSdd = 2 };
 
 // What a workgroup needs to choose and to number its tiles, from one pass
@@ -122,8 +127,7 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
   int32_t most = 0, ca = 0, cb = 0;
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
-    if (64 * p >= num_experts) break;
-    const int32_t v = n[p] > 0 ? n[p] : 0;
+    const int32_t v = n[p] > 0 ? n[p] : 0;  // 0 past the experts
     rows += v;
     most = max(most, v);
     ca += Chunking<RA>::count(v);

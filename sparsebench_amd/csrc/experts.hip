@@ -14,7 +14,7 @@
 // rows, M = 32 R rows for the chunk's own R = ceil(rows / 32), with one row
 // of waves, each owning a column strip of all R 32-row groups, on the
 // LDS-DMA main loop (gemm_dma.hpp).
-//   SDD  chunks of up to 160 rows (RMAX 5: an expert with 129-160 rows is
+//   SDD  chunks of up to 192 rows (RMAX 6: an expert with 129-192 rows is
 //        one tile), 512 columns per tile, 8 waves of 64 columns.
 //   DSD  chunks of up to 256 rows (RMAX 8), 256 columns per tile, 4 waves
 //        of 64 columns; at the fine-grained shape 64 experts x 4 slices is
@@ -49,9 +49,12 @@ namespace {
 
 // Main-loop configuration of an R-group tile: M = 32 R, K steps of 32, one
 // row of WAVES waves, non-temporal weight loads, DMA issue spread over the
-// MFMAs (PIPE 3).
+// MFMAs (PIPE 3). With 8 waves (two per SIMD, at most 256 registers each)
+// and six row groups, the 192 accumulators leave room for one set of A
+// fragments only (PIPE 4); a bf16 tile over 160 KB is staged in two parts.
 template <int R, int BN, int WAVES, int STAGES>
-using ChunkCfg = DmaCfg<32 * R, BN, 32, STAGES, 1, WAVES, 0, 2, 3>;
+using ChunkCfg = DmaCfg<32 * R, BN, 32, STAGES, 1, WAVES, 0, 2, (WAVES == 8 && R >= 6) ? 4 : 3,
+                        (32 * R * BN * 2 > 160 * 1024) ? 2 : 1>;
 
 // LDS of the expert tiles of a kernel: the largest over its tile heights.
 template <int BN, int WAVES, int STAGES, int R>
@@ -130,22 +133,25 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
   typename ML::Acc acc;
   ML::run(lds, src, a.d_model / Cfg::BK, acc);
 
-  if (a.apply_gelu)
-    ML::stage_tile(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
-  else
-    ML::stage_tile(lds, acc, [](float v) { return v; });
   // Padded row p -> row block p / 128, whose blocks are (p / 128) * F/128 + f/128.
   const int64_t ffn_blocks = a.ffn_dim / kBS;
-  ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
-    const int p = ch.row0 + m;
-    const int f = n0 + col;
-    *reinterpret_cast<u32x4_t*>(a.out + ((p / kBS) * ffn_blocks + f / kBS) * (kBS * kBS) + (p % kBS) * kBS +
-                                (f % kBS)) = v;
+  static_for<0, Cfg::EPI_PARTS>([&](auto pc) {
+    constexpr int P = decltype(pc)::value;
+    if (a.apply_gelu)
+      ML::template stage_part<P>(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
+    else
+      ML::template stage_part<P>(lds, acc, [](float v) { return v; });
+    ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
+      const int p = ch.row0 + P * ML::kPartRows + m;
+      const int f = n0 + col;
+      *reinterpret_cast<u32x4_t*>(a.out + ((p / kBS) * ffn_blocks + f / kBS) * (kBS * kBS) + (p % kBS) * kBS +
+                                  (f % kBS)) = v;
+    });
   });
 }
 
-// Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 160 rows.
-constexpr int kSddBN = 512, kSddWaves = 8, kSddRmax = 5, kSddStages = 3;
+// Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 192 rows.
+constexpr int kSddBN = 512, kSddWaves = 8, kSddRmax = 6, kSddStages = 3;
 
 template <class CfgB, bool kFastGelu>
 __global__ void __launch_bounds__(64 * kSddWaves)
@@ -279,7 +285,10 @@ __global__ void __launch_bounds__(64 * kDsdWaves)
   uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, kDsdWaves, kDsdStages, kDsdRmax>(), CfgB::kLdsAlloc)];
   const LayoutSummary sum = summarize_layout<kDsdRmax, 4>(tokens_per_expert, num_experts);
   const DsdArgs a{h, w2, out, h_bytes, ffn_dim, d_model};
-  if (!expert_stage_runs(sum, num_experts, kGateDsd, force)) {
+  // The grid may hold fewer workgroups than expert tiles (see the launch):
+  // then the row blocks take the stage.
+  const bool fits = static_cast<int64_t>(sum.chunks_a) * (d_model / kDsdBN) <= static_cast<int64_t>(gridDim.x);
+  if (!(expert_stage_runs(sum, num_experts, kGateDsd, force) && (fits || force == 1))) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in order.
     const int blocks = sum.chunks_b;
     const int slices = d_model / CfgB::BN;
@@ -343,17 +352,41 @@ int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, 
       ffn_dim, num_experts, max_row_blocks, apply_gelu, force, stream);
 }
 
+// CUs of the current device, read once per device.
+int device_cus(int* cus_out) {
+  constexpr int kMaxDevices = 64;
+  static int cus[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(SB_ERR_HIP, "dsd_experts: no current device");
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return fail(SB_ERR_HIP, "dsd_experts: cannot read the CU count");
+    cus[dev] = n;
+  }
+  *cus_out = cus[dev];
+  return SB_OK;
+}
+
 template <class CfgB>
 int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
                      const int32_t* row_block_expert, void* out, int64_t max_row_blocks, int64_t num_experts,
                      int64_t num_copies, int64_t ffn_dim, int64_t d_model, int32_t force, hipStream_t stream) {
-  // Enough workgroups for either tiling, and few more: workgroups past the
-  // chosen tiling's tiles still read the counts before they return. Expert
-  // e's ceil(n_e / 256) chunks are at most 1 + (n_e - 1) / 256, so there
-  // are at most min(E, N) + N / 256 of them for N routed rows.
+  // Workgroups: every row-block tile, or every expert tile up to four per
+  // CU if they can be more, and no more: workgroups past the chosen
+  // tiling's tiles still read the counts before they return. Expert e's
+  // ceil(n_e / 256) chunks are at most 1 + (n_e - 1) / 256, so there are at
+  // most min(E, N) + N / 256 of them for N routed rows. Expert tiles the
+  // grid cannot hold would leave the rest to the row blocks (on the device).
+  int cus = 0;
+  if (const int rc = device_cus(&cus)) return rc;
   const int64_t rows = std::min(num_copies, max_row_blocks * kBS);
   const int64_t chunk_bound = std::min(max_row_blocks, std::min(num_experts, rows) + rows / (32 * kDsdRmax));
-  const int64_t tiles = std::max(chunk_bound * (d_model / kDsdBN), max_row_blocks * (d_model / CfgB::BN));
+  const int64_t expert_tiles = chunk_bound * (d_model / kDsdBN);
+  const int64_t forced_expert = expert_gate_override() == 1 ? expert_tiles : 0;
+  const int64_t tiles = std::max({std::min<int64_t>(expert_tiles, 4 * static_cast<int64_t>(cus)), forced_expert,
+                                  max_row_blocks * (d_model / CfgB::BN)});
   const int64_t h_bytes = max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2;
   dsd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kDsdWaves, 0, stream>>>(
       static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w2), tokens_per_expert, padded_offsets,

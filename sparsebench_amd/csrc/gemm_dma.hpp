@@ -70,12 +70,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 // sets without the pinned interleave. 3: as 1, and the DMA of the step
 // STAGES-1 ahead is issued among the MFMAs too, not as a burst after the
 // barrier (a burst of DMA instructions holds each wave at issue until the
-// address unit takes them, which delays its MFMAs).
-template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0, int PIPE_ = 0>
+// address unit takes them, which delays its MFMAs). 4: as 3 with the A
+// fragments single-buffered: each is read again for the next sub-step
+// right after its last MFMA of this one (TM x 4 fewer registers, for tall
+// tiles whose accumulators leave no room for a second set).
+// EPI_PARTS: the epilogue stages the bf16 tile through LDS in this many
+// parts of BM / EPI_PARTS rows (a 192 x 512 tile does not fit at once).
+template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0, int PIPE_ = 0,
+          int EPI_PARTS_ = 1>
 struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_;
   static constexpr int CPA = CPA_, CPB = CPB_;
   static constexpr int PIPE = PIPE_;
+  static constexpr int EPI_PARTS = EPI_PARTS_;
   static constexpr int WM = WM_, WN = WN_;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
@@ -93,9 +100,10 @@ struct DmaCfg {
   static constexpr int kBBytes = BK * kBRowBytes;
   static constexpr int kStageBytes = kABytes + kBBytes;
   static constexpr int kLdsBytes = STAGES * kStageBytes;
-  // LDS of a kernel: the ring, or the bf16 output tile staged through it in
-  // the epilogue if that is larger.
-  static constexpr int kLdsAlloc = kLdsBytes > BM * BN * 2 ? kLdsBytes : BM * BN * 2;
+  // LDS of a kernel: the ring, or the part of the bf16 output tile staged
+  // through it in the epilogue if that is larger.
+  static constexpr int kStagedPartBytes = BM * BN * 2 / EPI_PARTS;
+  static constexpr int kLdsAlloc = kLdsBytes > kStagedPartBytes ? kLdsBytes : kStagedPartBytes;
   static constexpr int kBInstr = kBBytes / 1024 / kWaves;
   static constexpr int kLoadsPerStep = kAInstr + kBInstr;
   static constexpr int kARowsPerInstr = 1024 / kARowBytes;
@@ -110,6 +118,7 @@ struct DmaCfg {
   static_assert(STAGES >= 2 && STAGES <= 8, "STAGES");
   static_assert(kLdsAlloc <= 160 * 1024, "LDS");
   static_assert(kLoadsPerStep * (STAGES - 2) <= 63, "vmcnt");
+  static_assert(EPI_PARTS == 1 || (WM == 1 && TM % EPI_PARTS == 0), "epilogue parts of whole row groups");
 };
 
 // A rows are BK/8 16-byte chunks: logical chunk c of row r sits at c ^ swz_a(r).
@@ -312,6 +321,35 @@ struct DmaMainloop {
         for (int i = 0; i < Cfg::TM; ++i)
           acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[jn], a[i], acc[jn][i], 0, 0, 0);
     };
+    if constexpr (Cfg::PIPE == 4) {
+      constexpr int kDma = __is_same(Dma, NoDma) ? 0 : Cfg::kLoadsPerStep;
+      auto read_a1 = [&](int sub, int i) {
+        return *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * sub + h) ^ a_swz[i]) << 4));
+      };
+      bf16x8_t a[Cfg::TM], b[2][Cfg::TN];
+      read_a(0, a);
+      read_b(0, b[0]);
+      static_for<0, kSub>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        if constexpr (s + 1 < kSub) read_b(s + 1, b[(s + 1) & 1]);
+        static_for<0, Cfg::TM>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+#pragma unroll
+          for (int jn = 0; jn < Cfg::TN; ++jn)
+            acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[s & 1][jn], a[i], acc[jn][i], 0, 0, 0);
+          if constexpr (s + 1 < kSub) a[i] = read_a1(s + 1, i);
+          // This sub-step's share of the DMA, spread over its row groups.
+          constexpr int q0 = s * kDma / kSub + i * (kDma / kSub) / Cfg::TM;
+          constexpr int q1 = s * kDma / kSub + (i + 1 == Cfg::TM ? kDma / kSub : (i + 1) * (kDma / kSub) / Cfg::TM);
+#pragma unroll
+          for (int q = q0; q < q1; ++q) dma(q);
+        });
+      });
+      // Whatever the division leaves over.
+#pragma unroll
+      for (int q = kSub * (kDma / kSub); q < kDma; ++q) dma(q);
+      return;
+    }
     if constexpr (Cfg::PIPE == 3) {
       constexpr int kMfma = Cfg::TM * Cfg::TN;
       constexpr int kReads = Cfg::TM + 2 * Cfg::TN;
@@ -387,7 +425,7 @@ struct DmaMainloop {
 #pragma unroll
     for (int s = 0; s < Cfg::STAGES - 1; ++s)
       if (s < num_steps) issue(lds, s, s, src);
-    if constexpr (Cfg::PIPE == 3) {
+    if constexpr (Cfg::PIPE == 3 || Cfg::PIPE == 4) {
       // Steps that issue a later step's loads, among their MFMAs; at the top
       // of each, steps t .. t+STAGES-2 are outstanding.
       int t = 0;
@@ -495,8 +533,10 @@ struct DmaMainloop {
   // stores whole row segments. The ring is free once the last step has been
   // computed; the caller passes its base. fn(v) maps an fp32 result
   // (activation, or identity) before rounding to bf16.
-  static constexpr int kStagedBytes = Cfg::BM * Cfg::BN * 2;
+  static constexpr int kStagedBytes = Cfg::kStagedPartBytes;
   static_assert(kStagedBytes <= Cfg::kLdsAlloc, "staged tile fits the kernel's LDS");
+  static constexpr int kPartGroups = Cfg::TM / Cfg::EPI_PARTS;  // 32-row groups per part (WM == 1 when split)
+  static constexpr int kPartRows = Cfg::BM / Cfg::EPI_PARTS;
   static_assert(Cfg::BN >= 128, "16 chunks per row at least");
 
   __device__ __forceinline__ static int staged_offset(int r, int chunk) {
@@ -505,12 +545,20 @@ struct DmaMainloop {
 
   template <class Fn>
   __device__ __forceinline__ static void stage_tile(uint8_t* __restrict__ lds, Acc& acc, Fn fn) {
-    __syncthreads();  // every wave is done reading the ring
+    static_assert(Cfg::EPI_PARTS == 1, "split epilogue: stage_part");
+    stage_part<0>(lds, acc, fn);
+  }
+
+  // Part P of the tile: its row groups P * kPartGroups .. +kPartGroups,
+  // staged as rows 0 .. kPartRows of LDS.
+  template <int P, class Fn>
+  __device__ __forceinline__ static void stage_part(uint8_t* __restrict__ lds, Acc& acc, Fn fn) {
+    __syncthreads();  // every wave is done reading the ring (or the previous part)
 #pragma unroll
     for (int jn = 0; jn < Cfg::TN; ++jn)
 #pragma unroll
-      for (int i = 0; i < Cfg::TM; ++i) {
-        const int m = out_row(i);
+      for (int i = P * kPartGroups; i < (P + 1) * kPartGroups; ++i) {
+        const int m = out_row(i) - P * kPartRows;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int n = out_col(jn, g);
@@ -529,7 +577,7 @@ struct DmaMainloop {
   template <class Fn>
   __device__ __forceinline__ static void for_each_staged_chunk(const uint8_t* __restrict__ lds, Fn fn) {
     constexpr int kChunksPerRow = Cfg::BN / 8;
-    constexpr int kChunks = Cfg::BM * kChunksPerRow;
+    constexpr int kChunks = kPartRows * kChunksPerRow;
     static_assert(kChunks % Cfg::kThreads == 0, "whole passes");
 #pragma unroll
     for (int q0 = 0; q0 < kChunks; q0 += Cfg::kThreads) {

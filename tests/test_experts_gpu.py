@@ -14,7 +14,7 @@ per-row-block kernels are themselves pinned to the oracle (test_sdd_gpu.py,
 test_dsd_gpu.py); one oracle check per variant is repeated here.
 
 The routings put experts on every side of the chunking's edges: 0, 1, 31,
-32, 33, 127, 128, 129, 160 (one 160-row tile), 161 (two tiles), 192, 255,
+32, 33, 127, 128, 129, 160, 161, 192 (one 192-row SDD tile), 193 (two), 255,
 256, 257 (a 256-row tile plus one more) and several blocks; more than 64
 experts make the in-kernel chunk search take several passes.
 """
@@ -33,8 +33,8 @@ pytestmark = pytest.mark.gpu
 
 TOL = {"rtol": 1.6e-2, "atol": 1.6e-2}
 GATES = ["0", "1", "2"]  # choose on the device / expert tiles / row blocks
-SDD_RMAX = 5  # the SDD expert tiles hold up to 160 rows
-EDGE_COUNTS = [0, 1, 31, 32, 33, 127, 128, 129, 160, 161, 192, 255, 256, 257, 300, 600, 0, 5]
+SDD_RMAX = 6  # the SDD expert tiles hold up to 192 rows
+EDGE_COUNTS = [0, 1, 31, 32, 33, 127, 128, 129, 160, 161, 192, 193, 255, 256, 257, 300, 600, 0, 5]
 
 
 def edge_routing(seed: int) -> torch.Tensor:
@@ -54,6 +54,8 @@ CASES = {
     # The fine-grained shape's routing (every expert <= 160 rows with this
     # seed) and F: 64 x 8 expert SDD tiles, 2 rounds on 256 CUs.
     "uniform_wide": (lambda s: routing_case("random", 4096, 64, seed=1), 64, 256, 4096),
+    # 1024 rows per expert: the SDD keeps row blocks, the DSD takes chunks.
+    "few_experts": (lambda s: routing_case("random", 2048, 4, seed=s), 4, 256, 512),
 }
 
 

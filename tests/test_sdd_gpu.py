@@ -94,6 +94,40 @@ def test_sdd_wide_tiles() -> None:
     torch.testing.assert_close(run_sdd(idx, x, w1).float().cpu(), expected(idx, x, w1), **TOL)
 
 
+@pytest.mark.parametrize("entry", ["sdd", "sdd_experts"])
+def test_gelu_values_are_pinned(entry: str) -> None:
+    # x = I makes each pre-activation exactly one W1 value (token t reads row
+    # t of W1 alone), so H[t, f] = bf16(GELU(W1[t, f])) for 131072 chosen
+    # values in [-6, 6]. Expected: the erf form in fp64 (torch), rounded to
+    # bf16. The kernel's erfc approximation (|error| <= 1.5e-7) rounds to
+    # the same bf16 on [-3, 6] save a few ties; below -3 GELU is under 4e-3
+    # and only its absolute error is small. The tanh form matches about 85%
+    # of these values, and one dropped polynomial term about 39%.
+    from sparsebench_amd import _C
+    from sparsebench_amd.routing import route_device
+    from sparsebench_amd.spmm import sdd
+
+    t = d = 256
+    f = 512
+    v = torch.linspace(-6.0, 6.0, d * f).bfloat16().view(1, d, f)
+    x = torch.eye(t, d).bfloat16()
+    topo = route_device(torch.zeros(t, 1, dtype=torch.int64, device="cuda"), 1, f, 128)
+    if entry == "sdd":
+        h = sdd(x.cuda(), v.cuda(), topo, gelu=True)
+    else:
+        h = _C.sdd_experts_cuda(x.cuda(), v.cuda(), topo, True)
+    # One expert, tokens in order: row block rb holds tokens 128 rb .. 128 rb + 127.
+    got = h[: (t // 128) * (f // 128)].view(t // 128, f // 128, 128, 128).permute(0, 2, 1, 3).reshape(t, f)
+    got = got.float().cpu()
+    want = torch.nn.functional.gelu(v[0].double()).float().bfloat16().float()
+    vals = v[0].float()
+    assert torch.all((got - want).abs() <= torch.clamp(want.abs() * 2.0**-7, min=1e-6)), "more than 1 bf16 ulp off"
+    core = vals >= -3.0
+    exact = (got[core] == want[core]).float().mean().item()
+    assert exact >= 0.999, f"only {exact:.4%} of GELU values on [-3, 6] round to the erf form's bf16"
+    assert torch.all(got[vals == 0] == 0)
+
+
 BAD = {
     "fp32_x": (lambda x, w1: (x.float(), w1), "bfloat16"),
     "f_not_256": (lambda x, w1: (x, w1[:, :, :128].contiguous()), "multiple of 256"),

@@ -114,19 +114,26 @@ __device__ __forceinline__ int xcd_remap(int bid, int live) {
 // slice at a time, so the tiles that run together on one XCD cover a few
 // row blocks x a few slices and share both their A rows and their W columns
 // in that XCD's L2. Tiles past the live region map row block first.
+// All arguments are wave-uniform; the results are made so explicitly: the
+// integer divisions run on the vector unit, and a result left in a VGPR
+// stays live across the caller's main loop (the layer kernels, which use
+// all 512 registers, spilled it to scratch).
 __device__ __forceinline__ void tile_coords(int tile, int live_rb, int slices, int group, int* rb, int* slice) {
+  int r, s;
   if (tile >= live_rb * slices || group <= 1) {
-    *rb = tile / slices;
-    *slice = tile % slices;
-    return;
+    r = tile / slices;
+    s = tile % slices;
+  } else {
+    const int per_group = group * slices;
+    const int g = tile / per_group;
+    const int first = g * group;
+    const int size = min(group, live_rb - first);
+    const int local = tile - g * per_group;
+    r = first + local % size;
+    s = local / size;
   }
-  const int per_group = group * slices;
-  const int g = tile / per_group;
-  const int first = g * group;
-  const int size = min(group, live_rb - first);
-  const int local = tile - g * per_group;
-  *rb = first + local % size;
-  *slice = local / size;
+  *rb = __builtin_amdgcn_readfirstlane(r);
+  *slice = __builtin_amdgcn_readfirstlane(s);
 }
 
 // Number of leading row blocks that can hold work. The routing layout puts

@@ -40,6 +40,39 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
   return v;
 }
 
+// tokens_per_expert[base + lane] (0 past the experts) for one pass of 64
+// experts. The addresses are uniform, so these are scalar loads: after a
+// CU's first tile they hit its scalar cache, where per-lane vector loads
+// go to L2 each time (about a microsecond while the CU's DMA streams run,
+// before every tile's first load). v_writelane_b32 moves each value into
+// its lane (this compiler has no builtin for it; the asm is not volatile,
+// so the loads are still batched into wide scalar loads ahead of it). A
+// partial last pass uses per-lane loads.
+__device__ __forceinline__ int32_t expert_counts(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
+                                                 int base) {
+  int32_t n = 0;
+  base = __builtin_amdgcn_readfirstlane(base);  // uniform in every caller; said so for the scalar loads
+  if (base + 64 <= num_experts) {
+    // Wide loads (tokens_per_expert is 16-byte aligned, base a multiple
+    // of 64), issued together before the first value is used.
+    const int4* q = reinterpret_cast<const int4*>(tokens_per_expert + base);
+    int4 c[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) c[j] = q[j];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int32_t v[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        asm("v_writelane_b32 %0, %1, %2" : "+v"(n) : "s"(__builtin_amdgcn_readfirstlane(v[k])), "i"(4 * j + k));
+    }
+  } else {  // the last pass of an expert count that is not a multiple of 64
+    const int lane = threadIdx.x & 63;
+    if (base + lane < num_experts) n = tokens_per_expert[base + lane];
+  }
+  return n;
+}
+
 struct Chunk {
   int32_t expert;  // -1: no such chunk
   int32_t row0;    // first padded row (a multiple of 128)
@@ -51,12 +84,10 @@ struct Chunk {
 template <int RMAX>
 __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_per_expert,
                                             const int32_t* __restrict__ padded_offsets, int32_t num_experts, int c) {
-  const int lane = threadIdx.x & 63;
   Chunk ch{-1, 0, 0, 0};
   int before = 0;  // chunks of the experts before this pass
   for (int base = 0; base < num_experts; base += 64) {
-    const int e = base + lane;
-    const int32_t n = e < num_experts ? tokens_per_expert[e] : 0;
+    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
     const int cc = Chunking<RMAX>::count(n);
     const int incl = wave_inclusive_scan(cc);
     const uint64_t reach = __ballot(before + incl > c);  // experts whose chunks run past c
@@ -113,21 +144,12 @@ struct LayoutSummary {
 template <int RA, int RB>
 __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restrict__ tokens_per_expert,
                                                           int32_t num_experts) {
-  // All loads first (one per 64 experts, each behind a uniform branch), so
-  // they are in flight together: this runs before every tile's first DMA.
-  constexpr int kPasses = 1024 / 64;  // routing allows up to 1024 experts
-  const int lane = threadIdx.x & 63;
-  int32_t n[kPasses];
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    n[p] = 0;
-    if (64 * p < num_experts && 64 * p + lane < num_experts) n[p] = tokens_per_expert[64 * p + lane];
-  }
   int64_t rows = 0;
   int32_t most = 0, ca = 0, cb = 0;
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int32_t v = n[p] > 0 ? n[p] : 0;  // 0 past the experts
+#pragma unroll 1
+  for (int base = 0; base < num_experts; base += 64) {
+    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int32_t v = n > 0 ? n : 0;
     rows += v;
     most = max(most, v);
     ca += Chunking<RA>::count(v);

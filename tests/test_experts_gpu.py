@@ -193,6 +193,27 @@ def test_moe_forward_expert_tiles_bit_identical(monkeypatch, case: str, gate: st
     assert torch.equal(moe_forward(*args), ref)
 
 
+@pytest.mark.parametrize(("config", "routing"),
+                         [("fine_grained", "random"), ("fine_grained", "zipf_perm"), ("mixtral", "random"),
+                          ("replay_sweep", "zipf_perm")])
+def test_full_size_layer_is_the_same_for_every_tiling(monkeypatch, config: str, routing: str) -> None:
+    # The benchmark configurations at their real sizes (the bench's inputs):
+    # the layer with the per-row-block kernels, with the device's choice,
+    # and with each tiling forced gives the same bits.
+    from sparsebench_amd.moe import moe_forward
+    from sparsebench_amd.workloads import SHAPES, make_layer
+
+    x, idx, gates, w1, w2 = make_layer(SHAPES[config], routing, seed=0)
+    gates = gates.bfloat16()
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    ref = moe_forward(x, idx, gates, w1, w2)
+    assert torch.isfinite(ref.float()).all()
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
+    for gate in GATES:
+        monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+        assert torch.equal(moe_forward(x, idx, gates, w1, w2), ref), f"gate {gate}"
+
+
 @pytest.mark.parametrize("gate", GATES)
 def test_moe_forward_rounded_expert_tiles_bit_identical(monkeypatch, gate: str) -> None:
     from sparsebench_amd.moe import moe_forward_rounded

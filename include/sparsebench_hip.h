@@ -78,7 +78,10 @@ int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, i
  * on the layout's blocks. x [T, D] bf16, w1 [E, D, F] bf16, 16-byte aligned;
  * D % 64 == 0, F % 256 == 0; row_token has num_row_blocks*128 entries.
  * Rows with row_token < 0 are zero (no read of x); row blocks with
- * row_offsets[r] == row_offsets[r+1] are skipped and their blocks left unwritten. */
+ * row_offsets[r] == row_offsets[r+1] are skipped and their blocks left unwritten.
+ * gelu is the erf form in fp32 (erfc to 1.5e-7, Abramowitz & Stegun 7.1.26),
+ * then round to nearest even; gelu(+-0) = +0, gelu(+inf) = +inf, NaN stays
+ * NaN, and gelu(-inf) = 0 where the erf formula gives NaN. */
 int sb_sdd(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
            const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
            int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, void* stream);

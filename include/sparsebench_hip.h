@@ -105,7 +105,9 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
  * the experts hold at most 256 rows on average: an expert's weights
  * are then streamed once per chunk of up to 192 rows (SDD) or 256 rows
  * (DSD) instead of once per row block, and padding rows past the last
- * 32-row group are neither computed nor read.
+ * 32-row group are neither computed nor read. sb_sdd_experts calls sb_sdd
+ * itself when F % 512 != 0, or when max_row_blocks shows more than 256
+ * copies per expert (the row blocks would be chosen for all copies valid).
  * The layout arrays are sb_routing's outputs (or those of
  * sb_routing_assigned / sb_token_rounding); max_row_blocks is its
  * worst-case row block count and num_copies the length of its copy_row.

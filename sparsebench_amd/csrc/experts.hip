@@ -425,7 +425,15 @@ extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_
     return fail(SB_ERR_INVALID, "problem too large");
   const int32_t force = expert_gate_override();
   // The expert tiles are 512 wide; other widths take the per-row-block kernel.
-  if (ffn_dim % kSddBN != 0 || force == 2)
+  // So do layouts of more than 256 copies per expert on average: the worst-
+  // case row block count, floor((n + 127 E) / 128), bounds the copies n from
+  // below, and with n rows the device would choose the row blocks too. It
+  // could choose otherwise only if many copies were dropped (bad expert ids,
+  // tokens past valid_tokens); the real rows are the same bits either way,
+  // and the per-row-block kernel skips the summary every layer workgroup
+  // computes first.
+  const int64_t min_copies = max_row_blocks * kBS - num_experts * (kBS - 1);
+  if (ffn_dim % kSddBN != 0 || force == 2 || (force != 1 && min_copies > 256 * num_experts))
     return sb_sdd(x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
                   max_row_blocks, apply_gelu, stream);
   const hipStream_t s = as_stream(stream);

@@ -164,6 +164,11 @@ __global__ void __launch_bounds__(64 * kSddWaves)
   static_assert(CfgB::kThreads == 64 * kSddWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
   __shared__ __attribute__((aligned(1024)))
   uint8_t lds[max_int(chunk_lds_bytes<kSddBN, kSddWaves, kSddStages, kSddRmax>(), CfgB::kLdsAlloc)];
+  // Workgroups past both tilings' tiles leave before the summary: every
+  // chunk starts a row block of its own, so there are at most live row
+  // blocks x slices tiles either way.
+  const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
+  if (static_cast<int>(blockIdx.x) >= live_rb * (ffn_dim / kSddBN)) return;
   const LayoutSummary sum = summarize_layout<kSddRmax, 4>(tokens_per_expert, num_experts);
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
   if (!expert_stage_runs(sum, num_experts, kGateSdd, force)) {
@@ -283,6 +288,9 @@ __global__ void __launch_bounds__(64 * kDsdWaves)
   static_assert(CfgB::kThreads == 64 * kDsdWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
   __shared__ __attribute__((aligned(1024)))
   uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, kDsdWaves, kDsdStages, kDsdRmax>(), CfgB::kLdsAlloc)];
+  // As in the SDD: at most live row blocks x D/256 tiles either way.
+  const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
+  if (static_cast<int>(blockIdx.x) >= live_rb * (d_model / kDsdBN)) return;
   const LayoutSummary sum = summarize_layout<kDsdRmax, 4>(tokens_per_expert, num_experts);
   const DsdArgs a{h, w2, out, h_bytes, ffn_dim, d_model};
   // The grid may hold fewer workgroups than expert tiles (see the launch):

@@ -150,7 +150,8 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
   });
 }
 
-// Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 192 rows.
+// Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 192 rows;
+// tiles of up to 128 rows have a 4-stage ring (4 x 40 KB fits the 160 KB).
 constexpr int kSddBN = 512, kSddWaves = 8, kSddRmax = 6, kSddStages = 3;
 
 template <class CfgB, bool kFastGelu>
@@ -163,7 +164,9 @@ __global__ void __launch_bounds__(64 * kSddWaves)
                      int32_t apply_gelu, int32_t group, int32_t force) {
   static_assert(CfgB::kThreads == 64 * kSddWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
   __shared__ __attribute__((aligned(1024)))
-  uint8_t lds[max_int(chunk_lds_bytes<kSddBN, kSddWaves, kSddStages, kSddRmax>(), CfgB::kLdsAlloc)];
+  uint8_t lds[max_int(max_int(chunk_lds_bytes<kSddBN, kSddWaves, kSddStages, kSddRmax>(),
+                               chunk_lds_bytes<kSddBN, kSddWaves, 4, 4>()),
+                       CfgB::kLdsAlloc)];
   // Workgroups past both tilings' tiles leave before the summary: every
   // chunk starts a row block of its own, so there are at most live row
   // blocks x slices tiles either way.
@@ -198,7 +201,7 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     return;
   with_groups<kSddRmax>(ch.groups, [&](auto rc) {
     constexpr int R = decltype(rc)::value;
-    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, kSddStages>, kFastGelu>(lds, a, ch, slice * kSddBN);
+    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, (R <= 4 ? 4 : kSddStages)>, kFastGelu>(lds, a, ch, slice * kSddBN);
   });
 }
 

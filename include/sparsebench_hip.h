@@ -50,12 +50,12 @@ int sb_arch_probe(int32_t* out, int64_t n, void* stream);
 int sb_read_probe(const void* data, int64_t bytes, int32_t mode, uint32_t key, uint32_t* sink, void* stream);
 
 /* Worst-case sizes of the routing outputs for n = T*k copies
- * (csrc/routing.cu:306-311). Host-only arithmetic; returns SB_ERR_INVALID
+ * (csrc/routing.cu:213-216). Host-only arithmetic; returns SB_ERR_INVALID
  * when the problem does not fit int32 indexing. */
 int sb_routing_sizes(int64_t num_copies, int32_t num_experts, int32_t ffn_dim, int32_t block_size,
                      int64_t* max_row_blocks, int64_t* max_rows, int64_t* workspace_elems);
 
-/* Replaces build_topology_cuda (csrc/routing.cu:291-375, csrc/ops.hpp:20-21).
+/* Replaces build_topology_cuda (csrc/routing.cu:197-281, csrc/ops.hpp:20-21).
  * expert_idx: [T, k] int32 (idx_is_i64 = 0) or int64 (idx_is_i64 = 1).
  * Writes, for the worst-case sizes given by sb_routing_sizes:
  *   tokens_per_expert[E], padded_offsets[E+1], row_token[max_rows],
@@ -67,7 +67,7 @@ int sb_routing_sizes(int64_t num_copies, int32_t num_experts, int32_t ffn_dim, i
  * holding T' <= T, and copies of tokens >= T' are neither counted nor
  * flagged (copy_row = -1): a graph captured at T can replay at T' <= T.
  * Outputs are bit-identical to sparsebench/topology.py:build_topology on the
- * live part, with the past-the-end conventions of routing.cu:256-287. */
+ * live part, with the past-the-end conventions of routing.cu:162-193, 248-249. */
 int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, int32_t k, int32_t num_experts,
                int32_t ffn_dim, int32_t block_size, const int32_t* valid_tokens, int32_t* workspace,
                int32_t* tokens_per_expert, int32_t* padded_offsets, int32_t* row_token, int32_t* copy_row,
@@ -153,7 +153,7 @@ int sb_dsd_combine(const void* blocks, const void* w, const int32_t* row_offsets
 
 /* ---- Routing given as assignments (sparsebench/moe.py:59-91) ---------- */
 
-/* Replaces the routing of moe_forward_assigned (sparsebench/moe.py:77-82:
+/* Replaces the routing of moe_forward_assigned (sparsebench/moe.py:80-84:
  * route_device on expert_of_copy as [N, 1], then row_token remapped from
  * copy index to token). Copy c sends token_of_copy[c] (int32/int64) to
  * expert_of_copy[c] (int32/int64). The outputs are those of sb_routing with
@@ -199,14 +199,14 @@ int sb_router_sizes(int64_t num_tokens, int32_t num_experts, int32_t k, int32_t 
                     int32_t ffn_dim, int64_t* max_assignments, int64_t* max_row_blocks, int64_t* max_rows,
                     int64_t* workspace_elems);
 
-/* Replaces top_k_assignments (sparsebench/token_rounding.py:42-49):
+/* Replaces top_k_assignments (sparsebench/token_rounding.py:39-46):
  * scores [T, E] fp32 -> top_idx [T, k] int32, the k best experts of each
  * token in descending score order (equal scores: lower expert first), and
  * top_weight [T, k] fp32 = the picked scores over their sum. k <= 16. */
 int sb_router_topk(const float* scores, int64_t num_tokens, int32_t num_experts, int32_t k, int32_t* top_idx,
                    float* top_weight, void* stream);
 
-/* Replaces token_rounding (sparsebench/token_rounding.py:61-85), fused with
+/* Replaces token_rounding (sparsebench/token_rounding.py:58-81), fused with
  * the routing of moe_forward_assigned, with no host sync.
  * scores [T, E] fp32. Writes the rounded routing as a list in (token,
  * expert) order, capacity max_assignments (sb_router_sizes):

@@ -6,8 +6,8 @@ CPU baseline): the product path (sparsebench_amd) never imports it and has no
 CPU fallback.
 
     topology_ref  the block-sparse layout (integer work, numpy), restating
-                  sparsebench/topology.py:58-123 and the worst-case/past-the-end
-                  conventions of csrc/routing.cu:123-287; pinned by a
+                  sparsebench/topology.py:53-118 and the worst-case/past-the-end
+                  conventions of csrc/routing.cu:44-51, 125-132, 157-158, 162-193, 248-249; pinned by a
                   brute-force loop version, invariants and known answers.
     moe_ref       fp32/fp64 torch references of the layer and its stages,
                   restating sparsebench/reference.py:49-114 and

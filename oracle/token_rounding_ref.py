@@ -5,9 +5,9 @@ never does.
 
 Each function follows the reference file:line it names. Pinned by
 tests/test_oracle_token_rounding.py against:
-  - the reference tests' known answers (tests/test_token_rounding.py:12-15
+  - the reference tests' known answers (tests/test_token_rounding.py:13-16
     for round_counts, :18-33 for the hand-worked 8-token case);
-  - the reference tests' properties (tests/test_token_rounding.py:36-85):
+  - the reference tests' properties (tests/test_token_rounding.py:36-83):
     every count a multiple of the tile, each expert moved by at most half a
     tile, rounded-down experts keep only their best picks, rounded-up
     experts add the best non-picks, weights sum to 1, determinism;
@@ -17,7 +17,7 @@ tests/test_oracle_token_rounding.py against:
 Tie rules: top-k picks the lower expert index among equal scores (torch's
 topk leaves this unspecified; with continuous scores ties do not occur), and
 within an expert's column equal shifted scores rank by token index (the
-reference's stable sort, token_rounding.py:77).
+reference's stable sort, token_rounding.py:73).
 """
 
 from __future__ import annotations
@@ -37,7 +37,7 @@ class Assignments:
 
 
 def top_k(scores: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
-    """(top_s, top_i) [T, k], descending, equal scores to the lower index (scores.topk at token_rounding.py:44)."""
+    """(top_s, top_i) [T, k], descending, equal scores to the lower index (scores.topk at token_rounding.py:42)."""
     scores = np.asarray(scores, dtype=np.float32)
     order = np.argsort(-scores, axis=1, kind="stable")[:, :k]
     return np.take_along_axis(scores, order, axis=1), order.astype(np.int64)
@@ -52,7 +52,7 @@ def _sequential_row_sum(values: np.ndarray) -> np.ndarray:
 
 
 def top_k_assignments(scores: np.ndarray, k: int) -> Assignments:
-    """Plain top-k as a list; weight = picked score / sum of the picks (token_rounding.py:42-49)."""
+    """Plain top-k as a list; weight = picked score / sum of the picks (token_rounding.py:39-46)."""
     top_s, top_i = top_k(scores, k)
     num_tokens = top_s.shape[0]
     token = np.repeat(np.arange(num_tokens, dtype=np.int64), k)
@@ -61,7 +61,7 @@ def top_k_assignments(scores: np.ndarray, k: int) -> Assignments:
 
 
 def round_counts(counts: np.ndarray, tile: int, max_count: int) -> np.ndarray:
-    """Nearest multiple of `tile`, ties down, at most max_count // tile * tile (token_rounding.py:52-58)."""
+    """Nearest multiple of `tile`, ties down, at most max_count // tile * tile (token_rounding.py:49-55)."""
     counts = np.asarray(counts, dtype=np.int64)
     low = counts // tile * tile
     high = low + tile * (counts % tile > 0)
@@ -70,14 +70,14 @@ def round_counts(counts: np.ndarray, tile: int, max_count: int) -> np.ndarray:
 
 
 def shifted_scores(scores: np.ndarray, top_s: np.ndarray, top_i: np.ndarray) -> np.ndarray:
-    """Picks keep their score, every other entry drops by 1, in fp32 (token_rounding.py:72-74)."""
+    """Picks keep their score, every other entry drops by 1, in fp32 (token_rounding.py:67-70)."""
     shifted = (np.asarray(scores, dtype=np.float32) - np.float32(1.0)).astype(np.float32)
     np.put_along_axis(shifted, top_i, top_s, axis=1)
     return shifted
 
 
 def keep_mask(scores: np.ndarray, k: int, tile: int) -> tuple[np.ndarray, np.ndarray]:
-    """(keep [T, E] bool, target [E]) of token rounding (token_rounding.py:64-79)."""
+    """(keep [T, E] bool, target [E]) of token rounding (token_rounding.py:61-76)."""
     scores = np.asarray(scores, dtype=np.float32)
     num_tokens, num_experts = scores.shape
     top_s, top_i = top_k(scores, k)
@@ -91,7 +91,7 @@ def keep_mask(scores: np.ndarray, k: int, tile: int) -> tuple[np.ndarray, np.nda
 
 
 def token_rounding(scores: np.ndarray, k: int, tile: int = 128) -> Assignments:
-    """Every expert's count rounded to a multiple of `tile` (token_rounding.py:61-85).
+    """Every expert's count rounded to a multiple of `tile` (token_rounding.py:58-81).
 
     The list is in (token, expert) order (nonzero of the keep mask); weights
     are the kept scores over each token's kept total, summed in list order.
@@ -134,7 +134,7 @@ def brute_force_keep(scores: np.ndarray, k: int, tile: int) -> np.ndarray:
 
 
 def routing_change(scores: np.ndarray, k: int, rounded: Assignments, tile: int = 128) -> dict[str, float]:
-    """How far `rounded` is from plain top-k (token_rounding.py:88-111)."""
+    """How far `rounded` is from plain top-k (token_rounding.py:84-103)."""
     scores = np.asarray(scores, dtype=np.float32)
     num_tokens, num_experts = scores.shape
     _, top_i = top_k(scores, k)

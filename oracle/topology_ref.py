@@ -1,11 +1,11 @@
 """Block-sparse layout oracle (numpy, integer-exact). TEST INFRASTRUCTURE ONLY.
 
-Restates the algorithm of the reference's sparsebench/topology.py:58-123
+Restates the algorithm of the reference's sparsebench/topology.py:53-118
 (stable counting sort of copies by expert, padding to block_size, BSR with
 every row block holding its expert's ffn_blocks column blocks) and the
 device-side conventions of csrc/routing.cu: bad expert ids are skipped and
-flagged (routing.cu:138-145, 219-253), and the worst-case buffers are
-marked past the real end (routing.cu:256-287, 342-343).
+flagged (routing.cu:44-51, 125-132, 157-158), and the worst-case buffers are
+marked past the real end (routing.cu:162-193, 248-249).
 """
 
 from __future__ import annotations
@@ -44,13 +44,13 @@ class Layout:
 
 
 def worst_case_sizes(num_copies: int, num_experts: int, ffn_dim: int, block_size: int) -> tuple[int, int]:
-    """(max_row_blocks, max_rows): every expert wastes block_size - 1 rows (routing.cu:306-311)."""
+    """(max_row_blocks, max_rows): every expert wastes block_size - 1 rows (routing.cu:213-216)."""
     max_row_blocks = (num_copies + num_experts * (block_size - 1)) // block_size
     return max_row_blocks, max_row_blocks * block_size
 
 
 def _validate(expert_idx: np.ndarray, num_experts: int, ffn_dim: int, block_size: int) -> None:
-    # The checks of topology.py:62-72 (ValueError / TypeError).
+    # The checks of topology.py:57-67 (ValueError / TypeError).
     if expert_idx.ndim != 2 or expert_idx.shape[0] == 0 or expert_idx.shape[1] == 0:
         raise ValueError(f"expert_idx must be [T, k] with T, k > 0, got {tuple(expert_idx.shape)}")
     if expert_idx.dtype not in (np.int32, np.int64):
@@ -102,7 +102,7 @@ def build_layout(expert_idx: np.ndarray, num_experts: int, ffn_dim: int, block_s
 def device_layout(
     expert_idx: np.ndarray, num_experts: int, ffn_dim: int, block_size: int, valid_tokens: int | None = None
 ) -> Layout:
-    """The worst-case buffers of build_topology_cuda (routing.cu:291-375), every element.
+    """The worst-case buffers of build_topology_cuda (routing.cu:197-281), every element.
 
     Bad ids are skipped (copy_row = -1, not counted) and set error = 1;
     with valid_tokens = T', copies of tokens >= T' are skipped without error.

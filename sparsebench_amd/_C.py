@@ -112,7 +112,7 @@ def build_topology_cuda(
         _fail(f"ffn_dim ({ffn_dim}) must be a positive multiple of block_size ({block_size})")
     num_tokens, k = expert_idx.shape
     n = num_tokens * k
-    # Worst case: every expert wastes block_size - 1 rows (csrc/routing.cu:306-318).
+    # Worst case: every expert wastes block_size - 1 rows (csrc/routing.cu:213-224).
     max_row_blocks = (n + num_experts * (block_size - 1)) // block_size
     max_rows = max_row_blocks * block_size
     ffn_blocks = ffn_dim // block_size

@@ -3,8 +3,8 @@
 // A copy is one (token, choice) pair, c = t*k + j. Copies are sorted by
 // expert with a stable counting sort, padded per expert to a multiple of the
 // block size, and described as BSR for the two matmuls. The result is the
-// layout of sparsebench/topology.py:58-123 (reference), bit for bit, with the
-// worst-case buffer conventions of csrc/routing.cu:256-287.
+// layout of sparsebench/topology.py:53-118 (reference), bit for bit, with the
+// worst-case buffer conventions of csrc/routing.cu:162-193, 248-249.
 //
 // Three launches, all on the caller's stream:
 //   1. count    one workgroup per chunk of 1024 copies: per-expert counts of

@@ -1,5 +1,5 @@
 """The trimmed block-sparse layout (the Topology type of the reference's
-sparsebench/topology.py:30-55).
+sparsebench/topology.py:25-50).
 
 Copies (t, j) -> c = t*k + j are sorted by expert, each expert's group padded
 to a multiple of block_size. That gives P padded rows in row blocks of one
@@ -17,16 +17,17 @@ import torch
 class Topology:
     block_size: int
     num_experts: int
-    ffn_blocks: int  # F // block_size: column blocks per expert
+    ffn_blocks: int  # block columns of one expert's FFN (F / block_size)
 
-    tokens_per_expert: torch.Tensor  # [E] int32, real copies per expert
-    padded_offsets: torch.Tensor  # [E+1] int32, first padded row of each expert
-    row_token: torch.Tensor  # [P] int32, source token of each row, -1 = padding
-    copy_row: torch.Tensor  # [T*k] int32, padded row of copy (t, j) at t*k + j
+    # All int32. E experts, T*k copies, P padded rows.
+    tokens_per_expert: torch.Tensor  # [E]: copies routed to each expert
+    padded_offsets: torch.Tensor  # [E+1]: expert e's rows start at [e]; [E] = P
+    row_token: torch.Tensor  # [P]: token each row reads; padding rows hold -1
+    copy_row: torch.Tensor  # [T*k]: row that copy c = t*k + j landed in
 
-    row_block_expert: torch.Tensor  # [P / block_size] int32
-    row_offsets: torch.Tensor  # [P / block_size + 1] int32
-    col_indices: torch.Tensor  # [nnz_blocks] int32
+    row_block_expert: torch.Tensor  # [P / block_size]: owning expert per row block
+    row_offsets: torch.Tensor  # [P / block_size + 1]: BSR row pointers
+    col_indices: torch.Tensor  # [nnz]: block column of each stored block
 
     @property
     def num_rows(self) -> int:

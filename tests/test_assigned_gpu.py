@@ -1,7 +1,7 @@
 """The layer on a routing given as assignments, and the GPU router (top-k,
 token rounding fused with routing), against the CPU oracle.
 
-The cases of the reference's tests/test_token_rounding.py:88-148, plus:
+The cases of the reference's tests/test_token_rounding.py:91-148, plus:
 bit-exact router output (lists, weights, layout), the combine's list-order
 summation on both token-grouping paths, the token-rounded layer without a
 host sync under graph replay.
@@ -26,7 +26,7 @@ LAYER_TOL = {"rtol": 3e-2, "atol": 3e-2}
 
 
 def make_layer(num_tokens, num_experts, d_model=256, ffn_dim=256, seed=0):
-    # tests/test_token_rounding.py:102-107 (reference)
+    # tests/test_token_rounding.py:101-106 (reference)
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(num_tokens, d_model, generator=g).bfloat16().cuda()
     w1 = (torch.randn(num_experts, d_model, ffn_dim, generator=g) / d_model**0.5).bfloat16().cuda()
@@ -105,7 +105,7 @@ def test_token_rounding_exact(name, t, e, k, tile) -> None:
 
 
 def test_token_rounding_hand_worked_case() -> None:
-    # tests/test_token_rounding.py:18-33 (reference)
+    # tests/test_token_rounding.py:19-33 (reference)
     from sparsebench_amd.token_rounding import token_rounding
 
     s0 = torch.tensor([0.9, 0.8, 0.7, 0.6, 0.55, 0.1, 0.2, 0.3])
@@ -199,7 +199,7 @@ def test_token_csr(order, num_tokens, n) -> None:
 
 @pytest.mark.parametrize("name", ["uniform", "zipf"])
 def test_moe_assigned_with_token_rounding(name) -> None:
-    # tests/test_token_rounding.py:110-119 (reference)
+    # tests/test_token_rounding.py:109-120 (reference)
     from sparsebench_amd.moe import moe_forward_assigned
     from sparsebench_amd.token_rounding import token_rounding
 

@@ -1,7 +1,7 @@
 """Pins of the token-rounding oracle (oracle/token_rounding_ref.py), on the CPU.
 
 Known answers and properties are the reference's own tests
-(tests/test_token_rounding.py:12-85); the brute force ranks by counting,
+(tests/test_token_rounding.py:13-83); the brute force ranks by counting,
 with no sort, on small inputs with many ties.
 """
 
@@ -23,7 +23,7 @@ from sparsebench_amd.workloads import router_scores
 
 
 def test_round_counts_nearest_ties_down() -> None:
-    # tests/test_token_rounding.py:12-15 (reference)
+    # tests/test_token_rounding.py:13-16 (reference)
     counts = np.array([0, 1, 63, 64, 65, 128, 191, 192, 200])
     expected = np.array([0, 0, 0, 0, 128, 128, 128, 128, 256])
     assert np.array_equal(round_counts(counts, 128, 10_000), expected)
@@ -35,7 +35,7 @@ def test_round_counts_cap() -> None:
 
 
 def test_hand_worked_case() -> None:
-    # tests/test_token_rounding.py:18-33 (reference): 8 tokens, 2 experts,
+    # tests/test_token_rounding.py:19-33 (reference): 8 tokens, 2 experts,
     # k = 1, tile 4; expert 0 has 5 picks -> 4 (drops token 4), expert 1 has
     # 3 -> 4 (adds token 4, its best non-pick).
     s0 = np.array([0.9, 0.8, 0.7, 0.6, 0.55, 0.1, 0.2, 0.3], dtype=np.float32)
@@ -50,7 +50,7 @@ def test_hand_worked_case() -> None:
 @pytest.mark.parametrize("name", ["uniform", "zipf"])
 @pytest.mark.parametrize(("num_tokens", "num_experts", "k"), [(4096, 64, 2), (2000, 8, 2), (3000, 16, 4)])
 def test_properties(name: str, num_tokens: int, num_experts: int, k: int) -> None:
-    # tests/test_token_rounding.py:36-85 (reference)
+    # tests/test_token_rounding.py:36-83 (reference)
     tile = 128
     scores = router_scores(name, num_tokens, num_experts).numpy()
     rounded = token_rounding(scores, k, tile)

@@ -4,7 +4,7 @@
   (tests/test_topology.py:61-66, tests/test_routing.py:111-120 in the reference)
 - agreement with an independent brute-force construction on small inputs
 - the layout invariants of the reference's tests/test_topology.py:8-45
-- the worst-case / past-the-end conventions of csrc/routing.cu:256-287
+- the worst-case / past-the-end conventions of csrc/routing.cu:162-193, 248-249
 - the golden vectors under tests/golden/
 """
 

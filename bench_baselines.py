@@ -9,8 +9,6 @@ Layer pipelines (everything from the routing to the [T, D] output is timed,
 host syncs included):
   ours          moe_forward: GPU routing -> SDD (+ gather, GELU) -> DSD -> combine;
                 no host sync. Timed eagerly, and as a captured graph.
-  ours fused    moe_forward(fused_combine=True): the combine inside the DSD
-                kernel (same bits; graph).
   grouped_mm    sort copies by expert -> torch._grouped_mm -> GELU ->
                 torch._grouped_mm -> unsort -> weighted sum (torch ops, no sync).
   loop          per expert: x[tokens] @ w1[e] -> GELU -> @ w2[e], expert counts
@@ -31,7 +29,7 @@ moe_forward at T'.
 
 Ceilings (the box's practical roofs, next to the published 8 TB/s and
 2.5 PFLOP/s): streaming reads of 2 GiB with 16-byte vector loads and through
-LDS DMA (sb_read_probe, the load path of SDD / DSD), a 1 GiB device copy, and
+LDS DMA (sbp_read of libsparsebench_probe.so, the load path of SDD / DSD), a 1 GiB device copy, and
 dense bf16 GEMMs through torch.matmul (hipBLASLt).
 
 Every pipeline is checked against the fp32 loop reference before it is
@@ -132,9 +130,8 @@ def fmt(v) -> str:
 
 
 def layer_table(flush: torch.Tensor) -> list[str]:
-    lines = ["| shape | routing | ours (graph) | ours (eager) | ours fused combine (graph) | torch._grouped_mm | "
-             "per-expert loop |",
-             "|---|---|---:|---:|---:|---:|---:|"]
+    lines = ["| shape | routing | ours (graph) | ours (eager) | torch._grouped_mm | per-expert loop |",
+             "|---|---|---:|---:|---:|---:|"]
     print("\n".join(lines), flush=True)
     for shape_name in ("fine_grained", "mixtral"):
         shape = SHAPES[shape_name]
@@ -149,9 +146,6 @@ def layer_table(flush: torch.Tensor) -> list[str]:
             t_eager = checked(ours, ref, flush)
             t_graph = time_ms(graph_of(ours), flush) if isinstance(t_eager, float) else "-"
             row += [fmt(t_graph), fmt(t_eager)]
-            fused = lambda: moe_forward(x, idx, gates, w1, w2, fused_combine=True)  # noqa: E731
-            t_fused = checked(fused, ref, flush)
-            row.append(fmt(time_ms(graph_of(fused), flush)) if isinstance(t_fused, float) else fmt(t_fused))
             try:
                 row.append(fmt(checked(lambda: grouped_mm_layer(x, token, expert, weight, w1, w2), ref, flush)))
             except RuntimeError as e:
@@ -243,15 +237,36 @@ def replay_table(flush: torch.Tensor) -> list[str]:
     return lines
 
 
-def ceilings_table(flush: torch.Tensor) -> list[str]:
-    from sparsebench_amd import _C
+def read_probe():
+    """sbp_read of libsparsebench_probe.so (a measurement tool built beside the
+    library, not part of its C ABI): read a whole tensor once on the device."""
+    import ctypes
 
+    from sparsebench_amd import _lib
+
+    probe = ctypes.CDLL(str(_lib.LIB_PATH.with_name("libsparsebench_probe.so")))
+    probe.sbp_read.restype = ctypes.c_int
+    probe.sbp_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_void_p,
+                               ctypes.c_void_p]
+    probe.sbp_last_error.restype = ctypes.c_char_p
+
+    def run(data: torch.Tensor, mode: str, sink: torch.Tensor) -> None:
+        rc = probe.sbp_read(data.data_ptr(), data.numel() * data.element_size(), {"vector": 0, "lds_dma": 1}[mode],
+                            0x9E3779B9, sink.data_ptr(), _lib.stream_of(data.device))
+        if rc != 0:
+            raise RuntimeError(probe.sbp_last_error().decode())
+
+    return run
+
+
+def ceilings_table(flush: torch.Tensor) -> list[str]:
+    probe = read_probe()
     lines = ["| measurement | ms | rate | of published peak |", "|---|---:|---:|---:|"]
     print("\n".join(lines), flush=True)
     data = torch.ones(2 << 30, dtype=torch.uint8, device="cuda")
     sink = torch.zeros(256, dtype=torch.int32, device="cuda")
     for mode in ("vector", "lds_dma"):
-        ms = time_ms(lambda: _C.read_probe(data, mode, sink), flush)
+        ms = time_ms(lambda: probe(data, mode, sink), flush)
         tbs = data.numel() / ms / 1e9
         lines.append(f"| read 2 GiB, {mode} | {ms:.3f} | {tbs:.2f} TB/s | {tbs / 8.0:.0%} |")
         print(lines[-1], flush=True)

@@ -41,14 +41,6 @@ int32_t sb_version(void);
  * into out[0..n). n must be positive. */
 int sb_arch_probe(int32_t* out, int64_t n, void* stream);
 
-/* No counterpart in the reference: a measurement aid for the roofline.
- * Reads bytes of device memory at data (16-byte aligned) once, mode 0 with
- * 16-byte vector loads over a grid of 8 workgroups per CU, mode 1 through
- * LDS DMA (buffer_load ... lds) as the SDD / DSD main loops read, one
- * workgroup per MiB (bytes a multiple of 1 MiB). What is read is folded
- * into one word per lane, stored to sink[0..256) only if it equals key. */
-int sb_read_probe(const void* data, int64_t bytes, int32_t mode, uint32_t key, uint32_t* sink, void* stream);
-
 /* Worst-case sizes of the routing outputs for n = T*k copies
  * (csrc/routing.cu:213-216). Host-only arithmetic; returns SB_ERR_INVALID
  * when the problem does not fit int32 indexing. */
@@ -134,22 +126,6 @@ int sb_dsd_experts(const void* h, const void* w2, const int32_t* tokens_per_expe
 int sb_combine(const void* y, const int32_t* copy_row, const void* gates, int32_t gate_dtype, void* out,
                int64_t num_tokens, int32_t k, int64_t d_model, int64_t y_rows, const int32_t* valid_tokens,
                void* stream);
-
-/* Replaces the last two steps of moe_forward, dsd_cuda version 5 then the
- * combine (sparsebench/moe.py:48-54, csrc/dsd_v5.cu:106-123), with one
- * kernel. y [num_row_blocks*128, D] bf16 receives the DSD rows as sb_dsd
- * (zero_dead_rows = 0) writes them; out [T, D] bf16 receives exactly what
- * sb_combine(y, copy_row, gates, ...) would write, bit for bit: the tile
- * that writes a token's last routed row (per 256/512-column slice) sums the
- * token's rows in slot order. Tokens with no routed copy get a zero row.
- * Block size 128, D % 256 == 0; row_token / copy_row as sb_routing writes
- * them; gates [T, k] of gate_dtype; valid_tokens as for sb_combine.
- * counters: T * (D / 256) int32, all zero on entry and left zero on return;
- * two calls in flight at once must not share one counters buffer. */
-int sb_dsd_combine(const void* blocks, const void* w, const int32_t* row_offsets, const int32_t* col_indices,
-                   const int32_t* row_token, const int32_t* copy_row, const void* gates, int32_t gate_dtype, void* y,
-                   void* out, int32_t* counters, int64_t nnz, int64_t w_rows, int64_t num_row_blocks,
-                   int64_t d_model, int64_t num_tokens, int32_t k, const int32_t* valid_tokens, void* stream);
 
 /* ---- Routing given as assignments (sparsebench/moe.py:59-91) ---------- */
 

@@ -54,23 +54,6 @@ def arch_probe(n: int) -> torch.Tensor:
     return out
 
 
-READ_PROBE_MODES = {"vector": 0, "lds_dma": 1}
-
-
-def read_probe(data: torch.Tensor, mode: str, sink: torch.Tensor) -> None:
-    """Read all of `data` once on the device (a bandwidth probe; see
-    sb_read_probe): mode "vector" (16-byte loads) or "lds_dma" (whole MiB)."""
-    if not data.is_cuda or not data.is_contiguous():
-        _fail("read_probe: data must be a contiguous CUDA tensor")
-    if mode not in READ_PROBE_MODES:
-        _fail(f"read_probe: mode must be one of {sorted(READ_PROBE_MODES)}, got {mode!r}")
-    if sink.dtype != torch.int32 or sink.numel() < 256 or not sink.is_cuda:
-        _fail("read_probe: sink must be a CUDA int32 tensor of at least 256 elements")
-    nbytes = data.numel() * data.element_size()
-    check(lib().sb_read_probe(data.data_ptr(), nbytes, READ_PROBE_MODES[mode], 0x9E3779B9, sink.data_ptr(),
-                              stream_of(data.device)))
-
-
 def routing_sizes(num_copies: int, num_experts: int, ffn_dim: int, block_size: int) -> tuple[int, int, int]:
     """(max_row_blocks, max_rows, workspace int32 elements) for n = T*k copies."""
     rb, rows, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
@@ -534,67 +517,5 @@ def token_rounding_cuda(scores: torch.Tensor, k: int, tile: int, ffn_dim: int, b
     check(lib().sb_token_rounding(
         scores.data_ptr(), num_tokens, num_experts, k, tile, block_size, ffn_dim, workspace.data_ptr(),
         *(t.data_ptr() for t in out.values()), stream_of(dev),
-    ))
-    return out
-
-
-# Arrival counters of the fused DSD + combine, one zeroed buffer per
-# (device, size): each call leaves them zero again. Calls that overlap on
-# one device (two streams) would share them, as they share the GPU.
-_COMBINE_COUNTERS: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def _combine_counters(device: torch.device, n: int) -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), n)
-    buf = _COMBINE_COUNTERS.get(key)
-    if buf is None:
-        if torch.cuda.is_current_stream_capturing():
-            # A zero fill recorded into the graph would not run before the
-            # eager calls that share the buffer.
-            _fail("fused DSD + combine: call it once outside graph capture (allocates its counters)")
-        buf = torch.zeros(n, dtype=torch.int32, device=device)
-        _COMBINE_COUNTERS[key] = buf
-    return buf
-
-
-def dsd_combine_cuda(
-    blocks: torch.Tensor,
-    w: torch.Tensor,
-    row_offsets: torch.Tensor,
-    col_indices: torch.Tensor,
-    row_token: torch.Tensor,
-    copy_row: torch.Tensor,
-    expert_weight: torch.Tensor,
-    valid_tokens: torch.Tensor | None = None,
-) -> torch.Tensor:
-    """DSD (version 5 layout, block size 128) with the combine of moe_forward
-    fused into its epilogue: out [T, D] bf16, bit-identical to
-    combine_cuda(dsd_cuda(...), copy_row, expert_weight). No host sync."""
-    if not (blocks.is_cuda and w.is_cuda and expert_weight.is_cuda):
-        _fail("blocks, w and expert_weight must be CUDA tensors")
-    if blocks.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or not (blocks.is_contiguous() and w.is_contiguous()):
-        _fail("blocks and w must be contiguous bfloat16")
-    if not (blocks.dim() == 3 and blocks.shape[1] == blocks.shape[2] == 128):
-        _fail(f"dsd+combine needs blocks [nnz, 128, 128], got {_shape(blocks)}")
-    for t, name in ((row_offsets, "row_offsets"), (col_indices, "col_indices"), (row_token, "row_token"),
-                    (copy_row, "copy_row")):
-        _check_index(t, name)
-    if expert_weight.dim() != 2 or expert_weight.numel() != copy_row.numel():
-        _fail(f"expert_weight must be [T, k] with T*k == len(copy_row), got {_shape(expert_weight)}")
-    d_model = w.shape[1]
-    num_row_blocks = row_offsets.numel() - 1
-    if row_token.numel() != num_row_blocks * 128:
-        _fail("row_token must have one entry per row of the layout")
-    gates = expert_weight if expert_weight.dtype in _GATE_DTYPES else expert_weight.float()
-    gates = gates.contiguous()
-    num_tokens, k = expert_weight.shape
-    y = torch.empty(num_row_blocks * 128, d_model, dtype=w.dtype, device=w.device)
-    out = torch.empty(num_tokens, d_model, dtype=w.dtype, device=w.device)
-    counters = _combine_counters(w.device, num_tokens * max(1, d_model // 256))
-    check(lib().sb_dsd_combine(
-        blocks.data_ptr(), w.data_ptr(), row_offsets.data_ptr(), col_indices.data_ptr(), row_token.data_ptr(),
-        copy_row.data_ptr(), gates.data_ptr(), _GATE_DTYPES[gates.dtype], y.data_ptr(), out.data_ptr(),
-        counters.data_ptr(), blocks.shape[0], w.shape[0], num_row_blocks, d_model, num_tokens, k,
-        _ptr(valid_tokens), stream_of(w.device),
     ))
     return out

@@ -40,7 +40,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]
     ),
     "sb_dsd_experts": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr]),
-    "sb_read_probe": (_c_int, [_ptr, _i64, _i32, ctypes.c_uint32, _ptr, _ptr]),
     "sb_combine": (_c_int, [_ptr, _ptr, _ptr, _i32, _ptr, _i64, _i32, _i64, _i64, _ptr, _ptr]),
     "sb_routing_assigned": (
         _c_int,
@@ -55,11 +54,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.POINTER(_i64)],
     ),
     "sb_router_topk": (_c_int, [_ptr, _i64, _i32, _i32, _ptr, _ptr, _ptr]),
-    "sb_dsd_combine": (
-        _c_int,
-        [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr,
-         _ptr],
-    ),
     "sb_token_rounding": (
         _c_int,
         [_ptr, _i64, _i32, _i32, _i32, _i32, _i32, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,

@@ -3,7 +3,9 @@
     python -m sparsebench_amd.build
 
 Each .hip source is compiled to an object (in parallel) and linked into one
-shared library next to this file. The library links libamdhip64.so.7 by
+shared library next to this file. The read-bandwidth probe, a measurement
+tool and not part of the C ABI, is linked on its own into
+libsparsebench_probe.so. The library links libamdhip64.so.7 by
 soname; inside a Python process that has imported torch, that resolves to the
 HIP runtime torch already loaded, so there is one runtime per process.
 """
@@ -23,9 +25,11 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 BUILD = ROOT / "_build"
 LIB_NAME = "libsparsebench_hip.so"
+PROBE_LIB_NAME = "libsparsebench_probe.so"
 ARCH = "gfx950"
 
 SOURCES = ["probe.hip", "routing.hip", "sdd.hip", "dsd.hip", "combine.hip", "assigned.hip", "router.hip", "experts.hip"]
+PROBE_SOURCES = ["read_probe.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -60,25 +64,31 @@ def _compile(src: pathlib.Path, obj: pathlib.Path, extra: list[str]) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False, extra: list[str] | None = None) -> pathlib.Path:
-    """Compile every source and link the shared library. Returns its path."""
-    extra = list(extra or [])
-    BUILD.mkdir(exist_ok=True)
-    objs = [BUILD / (s.rsplit(".", 1)[0] + ".o") for s in SOURCES]
-    jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")))
-    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        futs = [pool.submit(_compile, CSRC / s, o, extra) for s, o in zip(SOURCES, objs)]
-        for f in futs:
-            f.result()
-    out = PKG / LIB_NAME
+def _link(objs: list[pathlib.Path], out: pathlib.Path) -> None:
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stderr}")
+        raise RuntimeError(f"link of {out.name} failed:\n{proc.stderr}")
     os.replace(tmp, out)
+
+
+def build(verbose: bool = False, extra: list[str] | None = None) -> pathlib.Path:
+    """Compile every source and link the shared libraries. Returns the product library's path."""
+    extra = list(extra or [])
+    BUILD.mkdir(exist_ok=True)
+    sources = SOURCES + PROBE_SOURCES
+    objs = {s: BUILD / (s.rsplit(".", 1)[0] + ".o") for s in sources}
+    jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        futs = [pool.submit(_compile, CSRC / s, objs[s], extra) for s in sources]
+        for f in futs:
+            f.result()
+    out = PKG / LIB_NAME
+    _link([objs[s] for s in SOURCES], out)
+    _link([objs[s] for s in PROBE_SOURCES], PKG / PROBE_LIB_NAME)
     if verbose:
-        print(f"built {out}")
+        print(f"built {out} and {PKG / PROBE_LIB_NAME}")
     return out
 
 

@@ -35,45 +35,18 @@ inline int check_launch(const char* what) {
   return SB_OK;
 }
 
-// Kernel-variant override from the environment, for tuning sweeps (read on
-// every call); 0 when unset, which selects the built-in choice.
-inline int tuning_override(const char* name) {
+// Test hook read from the environment on each call (0 when unset, which
+// keeps the built-in choice): SPARSEBENCH_EXPERT_GATE forces one tiling of
+// the layer kernels, SPARSEBENCH_TOPK_KERNEL one form of the top-k router.
+inline int env_override(const char* name) {
   const char* v = std::getenv(name);
   return v ? std::atoi(v) : 0;
 }
 
 // Row blocks per tile group (see tile_coords).
-inline int tile_group() {
-  const int forced = tuning_override("SPARSEBENCH_TILE_GROUP");
-  return forced > 0 ? forced : 8;
-}
+constexpr int kTileGroup = 8;
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
-
-// Grid of a persistent kernel: as many workgroups as the device holds at
-// once (CUs x resident workgroups per CU), at most `tiles`. The CU count is
-// read once per device and the occupancy once per kernel.
-inline int persistent_grid(const void* kernel, int threads, int64_t tiles, int* occupancy_cache, int* grid) {
-  constexpr int kMaxDevices = 64;
-  static int cus[kMaxDevices] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(SB_ERR_HIP, "persistent launch: no current device");
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      return fail(SB_ERR_HIP, "persistent launch: cannot read the CU count");
-    cus[dev] = n;
-  }
-  if (*occupancy_cache == 0) {
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, 0) != hipSuccess || occ <= 0)
-      return fail(SB_ERR_HIP, "persistent launch: kernel does not fit on a CU");
-    *occupancy_cache = occ;
-  }
-  *grid = static_cast<int>(std::min<int64_t>(tiles, static_cast<int64_t>(cus[dev]) * *occupancy_cache));
-  return SB_OK;
-}
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

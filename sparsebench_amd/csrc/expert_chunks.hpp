@@ -179,7 +179,7 @@ __device__ __forceinline__ bool expert_tiles_chosen(const LayoutSummary& sum, in
 // Host side of the gate: SPARSEBENCH_EXPERT_GATE=1 forces the expert
 // tiles, 2 the row blocks (for tests and tuning); 0 or unset chooses.
 inline int32_t expert_gate_override() {
-  const int v = tuning_override("SPARSEBENCH_EXPERT_GATE");
+  const int v = env_override("SPARSEBENCH_EXPERT_GATE");
   return v == 1 || v == 2 ? v : 0;
 }
 

@@ -108,7 +108,7 @@ struct SddArgs {
   int32_t apply_gelu;
 };
 
-template <class Cfg, bool kFastGelu>
+template <class Cfg>
 __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const SddArgs& a, const Chunk& ch, int n0) {
   using ML = DmaMainloop<Cfg>;
   SddChunkSrc<Cfg> src;
@@ -138,7 +138,7 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
   static_for<0, Cfg::EPI_PARTS>([&](auto pc) {
     constexpr int P = decltype(pc)::value;
     if (a.apply_gelu)
-      ML::template stage_part<P>(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
+      ML::template stage_part<P>(lds, acc, [](float v) { return gelu_erf_fast(v); });
     else
       ML::template stage_part<P>(lds, acc, [](float v) { return v; });
     ML::for_each_staged_chunk(lds, [&](int m, int col, u32x4_t v) {
@@ -154,7 +154,7 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
 // tiles of up to 128 rows have a 4-stage ring (4 x 40 KB fits the 160 KB).
 constexpr int kSddBN = 512, kSddWaves = 8, kSddRmax = 6, kSddStages = 3;
 
-template <class CfgB, bool kFastGelu>
+template <class CfgB>
 __global__ void __launch_bounds__(64 * kSddWaves)
     sdd_layer_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
                      const int32_t* __restrict__ row_token, const int32_t* __restrict__ row_block_expert,
@@ -185,7 +185,7 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     if (rb >= blocks || rb >= max_row_blocks) return;
     const int32_t expert = __builtin_amdgcn_readfirstlane(row_block_expert[rb]);
     if (expert < 0 || expert >= num_experts) return;
-    sdd_chunk_tile<CfgB, kFastGelu>(lds, a, Chunk{expert, rb * kBS, kBS, 4}, slice * CfgB::BN);
+    sdd_chunk_tile<CfgB>(lds, a, Chunk{expert, rb * kBS, kBS, 4}, slice * CfgB::BN);
     return;
   }
   const int chunks = sum.chunks_a;
@@ -201,7 +201,7 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     return;
   with_groups<kSddRmax>(ch.groups, [&](auto rc) {
     constexpr int R = decltype(rc)::value;
-    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, (R <= 4 ? 4 : kSddStages)>, kFastGelu>(lds, a, ch, slice * kSddBN);
+    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, (R <= 4 ? 4 : kSddStages)>>(lds, a, ch, slice * kSddBN);
   });
 }
 
@@ -331,7 +331,7 @@ __global__ void __launch_bounds__(64 * kDsdWaves)
 
 // --------------------------------------------------------------- launch ---
 
-template <class CfgB, bool kFastGelu>
+template <class CfgB>
 int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
                      const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
                      void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
@@ -340,27 +340,26 @@ int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, co
   // starts a row block of its own).
   static_assert(CfgB::BN == kSddBN, "one grid for both tilings");
   const int64_t tiles = max_row_blocks * (ffn_dim / kSddBN);
-  sdd_layer_kernel<CfgB, kFastGelu><<<static_cast<uint32_t>(tiles), 64 * kSddWaves, 0, stream>>>(
+  sdd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kSddWaves, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
       tokens_per_expert, padded_offsets, static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens),
       static_cast<int32_t>(d_model), static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts),
-      static_cast<int32_t>(max_row_blocks), apply_gelu, tile_group(), force);
+      static_cast<int32_t>(max_row_blocks), apply_gelu, kTileGroup, force);
   return check_launch("sdd_experts");
 }
 
-template <bool kFastGelu>
 int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
                        const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
                        void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
                        int64_t max_row_blocks, int32_t apply_gelu, int32_t force, hipStream_t stream) {
-  // The row-block tile is sb_sdd's default for the shape (default_sdd_variant).
-  if (default_sdd_variant(d_model, ffn_dim) == 62)
-    return launch_sdd_layer<DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 3>, kFastGelu>(
-        x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert, padded_offsets, out, num_tokens, d_model,
-        ffn_dim, num_experts, max_row_blocks, apply_gelu, force, stream);
-  return launch_sdd_layer<DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3>, kFastGelu>(
-      x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert, padded_offsets, out, num_tokens, d_model,
-      ffn_dim, num_experts, max_row_blocks, apply_gelu, force, stream);
+  // The row-block tile is sb_sdd's for the shape (sdd_tile_for).
+  if (sdd_tile_for(d_model, ffn_dim) == SddTile::kDeep)
+    return launch_sdd_layer<SddDeepTile>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
+                                         padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
+                                         max_row_blocks, apply_gelu, force, stream);
+  return launch_sdd_layer<SddWideTile>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
+                                       padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts, max_row_blocks,
+                                       apply_gelu, force, stream);
 }
 
 // CUs of the current device, read once per device.
@@ -403,7 +402,7 @@ int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_ex
       static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w2), tokens_per_expert, padded_offsets,
       row_block_expert, static_cast<uint16_t*>(out), h_bytes, static_cast<int32_t>(num_experts),
       static_cast<int32_t>(ffn_dim), static_cast<int32_t>(d_model), static_cast<int32_t>(max_row_blocks),
-      tile_group(), force);
+      kTileGroup, force);
   return check_launch("dsd_experts");
 }
 
@@ -430,9 +429,7 @@ extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_
     return fail(SB_ERR_INVALID, "sdd needs F (%lld) to be a multiple of 256", static_cast<long long>(ffn_dim));
   if (num_tokens <= 0 || num_tokens > kI32Max || num_experts <= 0 || num_experts > kMaxExperts)
     return fail(SB_ERR_INVALID, "sdd_experts: bad token or expert count");
-  if (num_tokens * d_model * 2 >= (int64_t{1} << 31) - 2 * d_model || ffn_dim * d_model * 2 >= (int64_t{1} << 31))
-    return fail(SB_ERR_INVALID, "sdd_experts: x or one expert's W1 too large for 32-bit buffer offsets");
-  if (max_row_blocks * kBS > kI32Max || max_row_blocks * (ffn_dim / kBS) > kI32Max)
+  if (ffn_dim * d_model > kI32Max || max_row_blocks * kBS > kI32Max || max_row_blocks * (ffn_dim / kBS) > kI32Max)
     return fail(SB_ERR_INVALID, "problem too large");
   const int32_t force = expert_gate_override();
   // The expert tiles are 512 wide; other widths take the per-row-block kernel.
@@ -442,19 +439,17 @@ extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_
   // could choose otherwise only if many copies were dropped (bad expert ids,
   // tokens past valid_tokens); the real rows are the same bits either way,
   // and the per-row-block kernel skips the summary every layer workgroup
-  // computes first.
+  // computes first. The layer kernel reads x and W1[e] through 32-bit buffer
+  // offsets; x of 2 GiB or more, or one expert's W1 of 2 GiB or more, also
+  // go to the per-row-block kernel, which gathers x with 64-bit addresses.
   const int64_t min_copies = max_row_blocks * kBS - num_experts * (kBS - 1);
-  if (ffn_dim % kSddBN != 0 || force == 2 || (force != 1 && min_copies > 256 * num_experts))
+  const bool offsets_fit = !sdd_wide_x(num_tokens, d_model) && ffn_dim * d_model * 2 < (int64_t{1} << 31);
+  if (ffn_dim % kSddBN != 0 || force == 2 || !offsets_fit || (force != 1 && min_copies > 256 * num_experts))
     return sb_sdd(x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
                   max_row_blocks, apply_gelu, stream);
-  const hipStream_t s = as_stream(stream);
-  const int rc = tuning_override("SPARSEBENCH_GELU_LIBM") > 0
-                     ? dispatch_sdd_layer<false>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
-                                                 padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
-                                                 max_row_blocks, apply_gelu, force, s)
-                     : dispatch_sdd_layer<true>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
-                                                padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
-                                                max_row_blocks, apply_gelu, force, s);
+  const int rc = dispatch_sdd_layer(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert, padded_offsets,
+                                    out, num_tokens, d_model, ffn_dim, num_experts, max_row_blocks, apply_gelu, force,
+                                    as_stream(stream));
   return rc ? rc : clear_ok();
 }
 

@@ -214,7 +214,14 @@ __device__ __forceinline__ void wait_steps(int later) {
 // Per-step sources, supplied by the kernel:
 //   a_src(t, &rsrc, &soffset), b_src(t, &rsrc, &soffset)
 // and fixed per-lane offsets a_voff(q), q < kAInstr, b_voff(q), q < kBInstr
-// (bytes).
+// (bytes). A source with kGlobalA = true gives A as per-lane 64-bit
+// addresses instead, a_global(q, t), loaded with global_load_lds (same LDS
+// destination, same vmcnt accounting).
+template <class Src, class = void>
+struct GlobalA : std::false_type {};
+template <class Src>
+struct GlobalA<Src, std::void_t<decltype(Src::kGlobalA)>> : std::bool_constant<Src::kGlobalA> {};
+
 template <class Cfg>
 struct DmaMainloop {
   using Acc = f32x16_t[Cfg::TN][Cfg::TM];  // acc[j][i]: C^T block (n block j, m block i)
@@ -232,8 +239,9 @@ struct DmaMainloop {
     __amdgpu_buffer_rsrc_t ra, rb;
     uint32_t sa, sb;
     const Src& src;
-    int wave;
-    __device__ __forceinline__ StepDma(uint8_t* __restrict__ stage_, int t, const Src& src_) : stage(stage_), src(src_) {
+    int wave, t;
+    __device__ __forceinline__ StepDma(uint8_t* __restrict__ stage_, int t_, const Src& src_)
+        : stage(stage_), src(src_), t(t_) {
       wave = threadIdx.x >> 6;
       src.a_src(t, &ra, &sa);
       src.b_src(t, &rb, &sb);
@@ -244,13 +252,17 @@ struct DmaMainloop {
       sb = __builtin_amdgcn_readfirstlane(sb);
     }
     __device__ __forceinline__ void operator()(int q) const {
-      if (q < Cfg::kAInstr)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024), 16,
-                                                 src.a_voff(q), sa, 0, Cfg::CPA);
-      else
+      if (q < Cfg::kAInstr) {
+        lds_void_t* dst = (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024);
+        if constexpr (GlobalA<Src>::value)
+          __builtin_amdgcn_global_load_lds(src.a_global(q, t), dst, 16, 0, Cfg::CPA);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst, 16, src.a_voff(q), sa, 0, Cfg::CPA);
+      } else {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q - Cfg::kAInstr) * 1024), 16,
             src.b_voff(q - Cfg::kAInstr), sb, 0, Cfg::CPB);
+      }
     }
   };
 

@@ -675,7 +675,7 @@ int launch_topk(const float* scores, int64_t num_tokens, int32_t num_experts, in
   // A lane per token unless its insertion work (E x the rounded-up k) is
   // large; SPARSEBENCH_TOPK_KERNEL=1 forces the wave form, 2 the lane form.
   const int kmax = k <= 1 ? 1 : k <= 2 ? 2 : k <= 4 ? 4 : k <= 8 ? 8 : 16;
-  const int forced = tuning_override("SPARSEBENCH_TOPK_KERNEL");
+  const int forced = env_override("SPARSEBENCH_TOPK_KERNEL");
   if (forced == 2 || (forced != 1 && kmax * num_experts <= 2048)) {
 #define SB_TOPK_LANE(K) \
   router_topk_lane_kernel<K><<<groups, 64, 0, s>>>(scores, num_tokens, num_experts, k, shifted, chunk_counts, top_idx, top_weight)

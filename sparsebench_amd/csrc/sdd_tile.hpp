@@ -9,17 +9,33 @@
 
 namespace sb {
 
-// The same tile on the LDS-DMA mainloop (gemm_dma.hpp): token rows are
-// gathered by the buffer loads themselves, padding rows read out of range
-// and land in LDS as zeros.
-template <class Cfg>
+// Sources of an SDD tile's K steps on the LDS-DMA main loop: token rows of
+// x gathered by the loads themselves, and W1[e] as stored.
+//
+// x under 2 GiB (kWideX false): one buffer over x; a lane's 32-bit offset is
+// its token row's chunk, and a padding row (no token) gets an out-of-range
+// offset, so the buffer unit lands zeros in LDS without reading memory.
+// x of 2 GiB or more (kWideX true): 32-bit offsets cannot reach every row,
+// so each lane issues global_load_lds from its own 64-bit address, its row's
+// chunk advanced by BK * 2 bytes per K step; a padding row's lane reads the
+// 16 zero bytes of sdd_zero_chunk at every step instead.
+static __device__ __attribute__((aligned(16))) uint32_t sdd_zero_chunk[4];
+
+template <class Cfg, bool kWideX = false>
 struct SddDmaSrc {
+  static constexpr bool kGlobalA = kWideX;
   __amdgpu_buffer_rsrc_t x_rsrc, w_rsrc;
   uint32_t a_off[Cfg::kAInstr];
   uint32_t b_off[Cfg::kBInstr];
   uint32_t b_step_bytes;
+  // Global form: this lane's address at step 0, and its advance per step.
+  uint64_t a_addr[kWideX ? Cfg::kAInstr : 1];
+  uint32_t a_step[kWideX ? Cfg::kAInstr : 1];
   __device__ __forceinline__ uint32_t a_voff(int q) const { return a_off[q]; }
   __device__ __forceinline__ uint32_t b_voff(int q) const { return b_off[q]; }
+  __device__ __forceinline__ const void* a_global(int q, int t) const {
+    return reinterpret_cast<const void*>(a_addr[q] + static_cast<uint64_t>(static_cast<uint32_t>(t)) * a_step[q]);
+  }
   __device__ __forceinline__ void a_src(int t, __amdgpu_buffer_rsrc_t* r, uint32_t* s) const {
     *r = x_rsrc;
     *s = static_cast<uint32_t>(t) * (Cfg::BK * 2);
@@ -28,13 +44,26 @@ struct SddDmaSrc {
     *r = w_rsrc;
     *s = static_cast<uint32_t>(t) * b_step_bytes;
   }
+  // Lane A position q reads token `tok` (< 0: a padding row), 16-byte chunk `chunk`.
+  __device__ __forceinline__ void set_row(int q, int32_t tok, int chunk, const uint16_t* x, int32_t d_model) {
+    if constexpr (kWideX) {
+      const bool real = tok >= 0;
+      a_addr[q] = real ? reinterpret_cast<uint64_t>(x + static_cast<int64_t>(tok) * d_model) + chunk * 16u
+                       : reinterpret_cast<uint64_t>(&sdd_zero_chunk[0]);
+      a_step[q] = real ? Cfg::BK * 2u : 0u;
+      a_off[q] = 0;
+    } else {
+      a_off[q] = tok >= 0 ? static_cast<uint32_t>(tok) * static_cast<uint32_t>(d_model) * 2u + chunk * 16u
+                          : kOutOfRange;
+    }
+  }
 };
 
 // Tile `tile_id` of the row-block grid: 128 rows x BN FFN columns of one
 // row block, written as BN/128 blocks. Ids past the grid's
 // num_row_blocks * num_slices tiles, dead row blocks and row blocks that are
 // not a routing layout's do nothing.
-template <class Cfg, bool kFastGelu>
+template <class Cfg, bool kWideX>
 __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, int tile_id,
                                                    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
                                                    const int32_t* __restrict__ row_token,
@@ -61,8 +90,8 @@ __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, in
       expert >= num_experts)
     return;
 
-  SddDmaSrc<Cfg> src;
-  src.x_rsrc = make_rsrc(x, static_cast<uint32_t>(num_tokens) * static_cast<uint32_t>(d_model) * 2u);
+  SddDmaSrc<Cfg, kWideX> src;
+  src.x_rsrc = make_rsrc(x, kWideX ? 0u : static_cast<uint32_t>(num_tokens) * static_cast<uint32_t>(d_model) * 2u);
   src.w_rsrc = make_rsrc(w1 + static_cast<int64_t>(expert) * d_model * ffn_dim,
                          static_cast<uint32_t>(d_model) * static_cast<uint32_t>(ffn_dim) * 2u);
   src.b_step_bytes = static_cast<uint32_t>(Cfg::BK) * static_cast<uint32_t>(ffn_dim) * 2u;
@@ -70,9 +99,7 @@ __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, in
 #pragma unroll
   for (int q = 0; q < Cfg::kAInstr; ++q) {
     const int32_t tok = row_token[static_cast<int64_t>(rb) * kBS + ap.row[q]];
-    src.a_off[q] = (tok >= 0 && tok < num_tokens)
-                        ? static_cast<uint32_t>(tok) * static_cast<uint32_t>(d_model) * 2u + ap.chunk[q] * 16u
-                        : kOutOfRange;
+    src.set_row(q, (tok >= 0 && tok < num_tokens) ? tok : -1, ap.chunk[q], x, d_model);
   }
   const BDmaPos<Cfg> bp;
 #pragma unroll
@@ -87,7 +114,7 @@ __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, in
   // stores: DSD reads H right after, and a non-temporal hint here makes SDD
   // alone faster but the layer slower (DSD then misses on H).
   if (apply_gelu)
-    ML::stage_tile(lds, acc, [](float v) { return kFastGelu ? gelu_erf_fast(v) : gelu_erf_libm(v); });
+    ML::stage_tile(lds, acc, [](float v) { return gelu_erf_fast(v); });
   else
     ML::stage_tile(lds, acc, [](float v) { return v; });
   uint16_t* blocks = out + static_cast<int64_t>(begin) * kBS * kBS;
@@ -97,13 +124,28 @@ __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, in
   });
 }
 
-// Default tile: 128 x 512 tiles of 8 waves (64 x 128 each), BK 32, a
-// 3-stage ring, or a 4-stage one for a deep reduction (D >= 4096); 128 x 256
-// tiles (BK 64 x 3 stages) when F is not a multiple of 512. From timing every
-// variant on the benchmark shapes (MI355X, samples interleaved).
-inline int default_sdd_variant(int64_t d_model, int64_t ffn_dim) {
-  if (ffn_dim % 512 != 0) return 63;
-  return d_model >= 4096 ? 62 : 65;
+// The tile shapes of the per-row-block SDD, from timing every shape tried on
+// the benchmark configurations (MI355X, samples interleaved across shapes):
+// 128 x 512 tiles of 8 waves (64 x 128 each: 8 MFMAs per 16-deep sub-step,
+// enough to cover the LDS fragment reads), BK 32 through a 3-stage ring, or
+// a 4-stage one for a deep reduction (D >= 4096); 128 x 256 tiles (BK 64 x 3
+// stages) when F is not a multiple of 512. All: non-temporal W1 loads, the
+// DMA of the step two ahead and the next sub-step's fragment reads issued
+// among the MFMAs (PIPE 3).
+using SddWideTile = DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3>;
+using SddDeepTile = DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 3>;
+using SddNarrowTile = DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 3>;
+
+enum class SddTile { kWide, kDeep, kNarrow };
+
+inline SddTile sdd_tile_for(int64_t d_model, int64_t ffn_dim) {
+  if (ffn_dim % 512 != 0) return SddTile::kNarrow;
+  return d_model >= 4096 ? SddTile::kDeep : SddTile::kWide;
+}
+
+// x of 2 GiB or more needs the 64-bit gather (SddDmaSrc's global form).
+inline bool sdd_wide_x(int64_t num_tokens, int64_t d_model) {
+  return num_tokens * d_model * 2 >= (int64_t{1} << 31) - 2 * d_model;
 }
 
 }  // namespace sb

@@ -71,7 +71,6 @@ def moe_forward(
     w2: torch.Tensor,
     mark: Callable[[str], None] = _no_mark,
     valid_tokens: torch.Tensor | None = None,
-    fused_combine: bool = False,
 ) -> torch.Tensor:
     """x [T, D], expert_idx / expert_weight [T, k], w1 [E, D, F], w2 [E, F, D] -> [T, D].
 
@@ -81,9 +80,6 @@ def moe_forward(
     restricts the layer to the first T' tokens without changing any shape,
     so a graph captured at T replays at any T' <= T; rows >= T' of the
     result are left unwritten.
-
-    fused_combine=True runs the combine inside the DSD kernel (the tile that
-    completes a token sums its rows; same bits as the separate combine).
     """
     num_experts, d_model, ffn_dim = w1.shape
     if w2.shape != (num_experts, ffn_dim, d_model):
@@ -93,16 +89,6 @@ def moe_forward(
 
     topo = route_device(expert_idx, num_experts, ffn_dim, BLOCK_SIZE, valid_tokens)
     mark("routing")
-    if fused_combine and d_model % 256 == 0:
-        h = sdd(x, w1, topo, gelu=True)
-        mark("SDD + GELU (fused)")
-        from sparsebench_amd import _C
-
-        out = _C.dsd_combine_cuda(h, w2.view(num_experts * ffn_dim, d_model), topo.row_offsets, topo.col_indices,
-                                  topo.row_token, topo.copy_row, expert_weight, valid_tokens)
-        mark("DSD")
-        mark("combine")
-        return out
     _, y = _sdd_dsd(x, w1, w2, topo, mark)
     out = combine(y, topo.copy_row, expert_weight, valid_tokens)
     mark("combine")

@@ -159,30 +159,3 @@ def test_assigned_entry_points_reject(lib) -> None:
     assert "weight dtype" in _err(lib)
     assert lib.sb_combine_assigned(p, p, p, 2, p, None, p, 1, 12, 4, None, None) == 1
     assert "multiple of 8" in _err(lib)
-
-
-def test_dsd_combine_rejects(lib) -> None:
-    buf = ctypes.create_string_buffer(64)
-    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
-    args = [p] * 7
-    assert lib.sb_dsd_combine(*args, 0, p, p, p, 2, 128, 1, 128, 4, 2, None, None) == 1
-    assert "multiple of 256" in _err(lib)
-    assert lib.sb_dsd_combine(*args, 0, p, p, None, 2, 128, 1, 256, 4, 2, None, None) == 1
-    assert "null buffer" in _err(lib)
-    assert lib.sb_dsd_combine(*args, 0, p, p, p, 2, 128, 1, 256, 0, 2, None, None) == 1
-    assert "token count" in _err(lib)
-    assert lib.sb_dsd_combine(*args, 7, p, p, p, 2, 128, 1, 256, 4, 2, None, None) == 1
-    assert "gate dtype" in _err(lib)
-
-
-def test_read_probe_rejects(lib) -> None:
-    buf = ctypes.create_string_buffer(64)
-    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
-    assert lib.sb_read_probe(p, 100, 0, 0, p, None) == 1
-    assert "multiple of 16" in _err(lib)
-    assert lib.sb_read_probe(p, 4096, 1, 0, p, None) == 1
-    assert "whole MiB" in _err(lib)
-    assert lib.sb_read_probe(p, 4096, 7, 0, p, None) == 1
-    assert "mode must be" in _err(lib)
-    assert lib.sb_read_probe(None, 4096, 0, 0, p, None) == 1
-    assert "null buffer" in _err(lib)

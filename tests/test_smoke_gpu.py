@@ -32,16 +32,3 @@ def test_one_hip_runtime_in_process() -> None:
     assert len(maps) == 1, maps
     libs = {ln.split()[-1] for ln in open("/proc/self/maps") if "libsparsebench_hip" in ln}
     assert len(libs) == 1, "the gfx950 library must be the one that ran"
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["vector", "lds_dma"])
-def test_read_probe_runs(mode) -> None:
-    from sparsebench_amd import _C
-
-    data = torch.arange(1 << 20, dtype=torch.int32, device="cuda")  # 4 MiB
-    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
-    _C.read_probe(data, mode, sink)
-    torch.cuda.synchronize()
-    with pytest.raises(RuntimeError, match="mode must be"):
-        _C.read_probe(data, "bogus", sink)

@@ -1,8 +1,17 @@
-"""Every SDD / DSD tile variant compiled into the library against the oracle.
+"""Every tile form the SDD / DSD drop-ins pick, against the oracle.
 
-The library picks one variant per shape; SPARSEBENCH_SDD_VARIANT /
-SPARSEBENCH_DSD_VARIANT select any other (for tuning). All must give the
-oracle's results to the same bf16 tolerance as the defaults (1.6e-2).
+sb_sdd / sb_dsd pick one tile form per shape (sdd_tile_for in sdd_tile.hpp,
+dispatch_dsd in dsd.hip). These tests reach each of them through the shape
+that selects it, for both block sizes of the DSD, and hold it to the bf16
+tolerance of the defaults (1.6e-2):
+
+  SDD  128 x 512, 3 stages (D < 4096, F % 512 == 0)   D 256, F 512
+       128 x 512, 4 stages (D >= 4096)                 D 4096, F 512
+       128 x 256 (F % 512 != 0)                        D 256, F 768
+  DSD  512 wide, 4 waves (D % 512 == 0, K < 8192)      D 512, K 256
+       512 wide, 8 waves (K = F per expert >= 8192)    D 512, K 8192
+       256 wide (D % 512 != 0, D % 256 == 0)           D 768
+       128 wide (D % 256 != 0)                         D 384
 """
 
 import math
@@ -17,108 +26,42 @@ from sparsebench_amd.workloads import routing_case
 pytestmark = pytest.mark.gpu
 
 TOL = {"rtol": 1.6e-2, "atol": 1.6e-2}
-COMMON = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 21, 22, 23, 24, 25, 26, 27, 31, 32, 33, 34,
-          35, 36, 37, 38, 39, 51, 52, 53, 54, 55, 56, 57, 58, 59, 61, 62, 63, 64, 65]
-SDD_PERSISTENT = [41, 43, 44]
-DSD_PERSISTENT = [41, 42, 43, 44, 45]
-SDD_VARIANTS = COMMON + SDD_PERSISTENT
-DSD_VARIANTS = COMMON + DSD_PERSISTENT
 
 
-@pytest.mark.parametrize("variant", SDD_VARIANTS)
+@pytest.mark.parametrize(("d_model", "ffn_dim"), [(256, 512), (4096, 512), (256, 768)], ids=["wide", "deep", "narrow"])
 @pytest.mark.parametrize("case", ["zipf", "empty_middle"])
-def test_sdd_variant(monkeypatch, variant: int, case: str) -> None:
+def test_sdd_tile_forms(d_model: int, ffn_dim: int, case: str) -> None:
     from sparsebench_amd.routing import route_device
     from sparsebench_amd.spmm import sdd
 
-    monkeypatch.setenv("SPARSEBENCH_SDD_VARIANT", str(variant))
-    g = torch.Generator().manual_seed(variant)
-    e, d, f, t = 8, 256, 512, 600
-    idx = routing_case(case, t, e, seed=variant)
-    x = torch.randn(t, d, generator=g).bfloat16()
-    w1 = (torch.randn(e, d, f, generator=g) / d**0.5).bfloat16()
-    dev = route_device(idx.cuda(), e, f, 128)
+    g = torch.Generator().manual_seed(d_model + ffn_dim)
+    e, t = 8, 600
+    idx = routing_case(case, t, e, seed=3)
+    x = torch.randn(t, d_model, generator=g).bfloat16()
+    w1 = (torch.randn(e, d_model, ffn_dim, generator=g) / d_model**0.5).bfloat16()
+    dev = route_device(idx.cuda(), e, ffn_dim, 128)
     out = sdd(x.cuda(), w1.cuda(), dev)
-    lay = build_layout(idx.numpy(), e, f, 128)
+    lay = build_layout(idx.numpy(), e, ffn_dim, 128)
     torch.testing.assert_close(out[: lay.col_indices.size].float().cpu(), sdd_blocks(x.float(), w1.float(), lay),
                                **TOL)
 
 
-@pytest.mark.parametrize("variant", DSD_VARIANTS)
+@pytest.mark.parametrize(("d_model", "ffn_dim"), [(512, 256), (512, 8192), (768, 256), (384, 256)],
+                         ids=["wide", "deep_k", "mid", "narrow"])
 @pytest.mark.parametrize("bs", [64, 128])
-def test_dsd_variant(monkeypatch, variant: int, bs: int) -> None:
+@pytest.mark.parametrize("version", [1, 4])
+def test_dsd_tile_forms(d_model: int, ffn_dim: int, bs: int, version: int) -> None:
     from sparsebench_amd import _C
 
-    monkeypatch.setenv("SPARSEBENCH_DSD_VARIANT", str(variant))
-    g = torch.Generator().manual_seed(100 + variant)
-    e, f, d = 8, 2 * bs, 512
-    lay = build_layout(routing_case("zipf", 500, e, seed=variant).numpy(), e, f, bs)
-    blocks = (torch.randn(lay.col_indices.size, bs, bs, generator=g) / math.sqrt(f)).bfloat16()
-    w = torch.randn(e * f, d, generator=g).bfloat16()
-    out = _C.dsd_cuda(blocks.cuda(), w.cuda(), torch.as_tensor(lay.row_offsets).cuda(),
-                      torch.as_tensor(lay.col_indices).cuda(), 4)
-    torch.testing.assert_close(out.float().cpu(), dsd_rows(blocks.float(), w.float(), lay), **TOL)
-
-
-# The persistent forms run about one workgroup per CU slot (256 on MI355X),
-# each walking several tiles with the DMA ring crossing tile boundaries.
-# These shapes give 2-6 tiles per workgroup, tiles of different experts in a
-# row, and dead row blocks after the live ones (worst-case buffers).
-
-
-@pytest.mark.parametrize("variant", SDD_PERSISTENT)
-@pytest.mark.parametrize("case", ["random", "zipf_perm"])
-def test_sdd_persistent_many_tiles(monkeypatch, variant: int, case: str) -> None:
-    from sparsebench_amd.routing import route_device
-    from sparsebench_amd.spmm import sdd
-
-    monkeypatch.setenv("SPARSEBENCH_SDD_VARIANT", str(variant))
-    g = torch.Generator().manual_seed(variant)
-    e, d, f, t = 64, 256, 1536, 4096
-    idx = routing_case(case, t, e, seed=variant)
-    x = torch.randn(t, d, generator=g).bfloat16()
-    w1 = (torch.randn(e, d, f, generator=g) / d**0.5).bfloat16()
-    dev = route_device(idx.cuda(), e, f, 128)
-    out = sdd(x.cuda(), w1.cuda(), dev)
-    lay = build_layout(idx.numpy(), e, f, 128)
-    torch.testing.assert_close(out[: lay.col_indices.size].float().cpu(), sdd_blocks(x.float(), w1.float(), lay),
-                               **TOL)
-
-
-@pytest.mark.parametrize("variant", DSD_PERSISTENT)
-@pytest.mark.parametrize("version", [1, 4])
-def test_dsd_persistent_many_tiles(monkeypatch, variant: int, version: int) -> None:
-    from sparsebench_amd.routing import route_device
-    from sparsebench_amd.spmm import dsd
-
-    monkeypatch.setenv("SPARSEBENCH_DSD_VARIANT", str(variant))
-    g = torch.Generator().manual_seed(200 + variant)
-    e, f, d, bs, t = 64, 256, 2048, 128, 4096
-    idx = routing_case("zipf_perm", t, e, seed=variant)
-    dev = route_device(idx.cuda(), e, f, bs)
-    blocks = (torch.randn(dev.col_indices.numel(), bs, bs, generator=g) / math.sqrt(f)).bfloat16()
-    w = torch.randn(e * f, d, generator=g).bfloat16()
-    out = dsd(blocks.cuda(), w.cuda(), dev, version=version)
-    lay = build_layout(idx.numpy(), e, f, bs)
+    g = torch.Generator().manual_seed(100 + d_model + bs)
+    e = 8
+    t = 300 if ffn_dim > 1024 else 500
+    lay = build_layout(routing_case("zipf", t, e, seed=5).numpy(), e, ffn_dim, bs)
+    blocks = (torch.randn(lay.col_indices.size, bs, bs, generator=g) / math.sqrt(ffn_dim)).bfloat16()
+    w = torch.randn(e * ffn_dim, d_model, generator=g).bfloat16()
+    # Worst-case buffers: two dead row blocks after the live ones.
+    row_offsets = torch.cat([torch.as_tensor(lay.row_offsets), torch.full((2,), int(lay.row_offsets[-1]))]).int()
+    out = _C.dsd_cuda(blocks.cuda(), w.cuda(), row_offsets.cuda(), torch.as_tensor(lay.col_indices).cuda(), version)
     torch.testing.assert_close(out[: lay.num_rows].float().cpu(), dsd_rows(blocks.float(), w.float(), lay), **TOL)
-    if version == 1:  # zeroes dead row blocks
+    if version == 1:  # versions 1-3 write dead row blocks as zeros
         assert torch.all(out[lay.num_rows:] == 0)
-
-
-@pytest.mark.parametrize("group", ["1", "3", "8", "64"])
-def test_tile_group_orders_agree(monkeypatch, group: str) -> None:
-    # The tile order changes which workgroup computes which tile, not the math:
-    # results are bit-identical for every group size.
-    from sparsebench_amd.moe import moe_forward
-
-    g = torch.Generator().manual_seed(7)
-    t, e, d, f = 700, 16, 256, 512
-    x = torch.randn(t, d, generator=g).bfloat16().cuda()
-    w1 = (torch.randn(e, d, f, generator=g) / d**0.5).bfloat16().cuda()
-    w2 = (torch.randn(e, f, d, generator=g) / f**0.5).bfloat16().cuda()
-    idx = routing_case("zipf", t, e).cuda()
-    gates = torch.rand(t, 2, generator=g).cuda()
-    monkeypatch.delenv("SPARSEBENCH_TILE_GROUP", raising=False)
-    ref = moe_forward(x, idx, gates, w1, w2)
-    monkeypatch.setenv("SPARSEBENCH_TILE_GROUP", group)
-    assert torch.equal(moe_forward(x, idx, gates, w1, w2), ref)

@@ -65,6 +65,22 @@ int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, i
                int32_t* tokens_per_expert, int32_t* padded_offsets, int32_t* row_token, int32_t* copy_row,
                int32_t* row_block_expert, int32_t* row_offsets, int32_t* col_indices, int32_t* error, void* stream);
 
+/* No counterpart in the reference: sb_routing for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments and outputs as sb_routing, without
+ * `workspace`: the per-chunk counts live in a fixed device array of
+ * 524288 int32 (2 MiB) that each GPU holds until the process ends. Problems
+ * that need more scratch (ceil(T*k / 1024) * (E + 1) int32, from
+ * sb_routing_sizes) are rejected with SB_ERR_INVALID. The first call on a
+ * device looks up that device's array (make it outside graph capture);
+ * no call allocates. Calls that overlap on one GPU share the array and
+ * race: issue them on one stream. */
+int sb_routing_noalloc(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, int32_t k,
+                       int32_t num_experts, int32_t ffn_dim, int32_t block_size, const int32_t* valid_tokens,
+                       int32_t* tokens_per_expert, int32_t* padded_offsets, int32_t* row_token, int32_t* copy_row,
+                       int32_t* row_block_expert, int32_t* row_offsets, int32_t* col_indices, int32_t* error,
+                       void* stream);
+
 /* Replaces sdd_cuda (csrc/sdd.cu:123-170, csrc/ops.hpp:34-36).
  * out[num_row_blocks*F/128, 128, 128] bf16 = (gelu)(x[row_token] @ w1[expert])
  * on the layout's blocks. x [T, D] bf16, w1 [E, D, F] bf16, 16-byte aligned;

@@ -34,6 +34,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_ptr, _i32, _i64, _i32, _i32, _i32, _i32, _ptr, _ptr,
          _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
     ),
+    "sb_routing_noalloc": (
+        _c_int,
+        [_ptr, _i32, _i64, _i32, _i32, _i32, _i32, _ptr,
+         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
+    ),
     "sb_sdd": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]),
     "sb_dsd": (_c_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i32, _ptr]),
     "sb_sdd_experts": (

@@ -17,6 +17,8 @@
 //               row_block_expert and mark every non-copy row -1.
 // Place's two roles touch disjoint memory and depend only on step 2.
 
+#include <mutex>
+
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -349,4 +351,75 @@ extern "C" int sb_routing_assigned(const void* expert_of_copy, int32_t expert_is
   const int rc = token_is_i64 ? run(static_cast<const int64_t*>(token_of_copy))
                               : run(static_cast<const int32_t*>(token_of_copy));
   return rc ? rc : clear_ok();
+}
+
+// ---- sb_routing_noalloc: sb_routing with its scratch in a fixed device array
+//
+// The only scratch of routing is the per-chunk expert counts that sb_routing
+// takes as `workspace` (ceil(n / 1024) * (E + 1) int32). This entry point
+// keeps them in `scratch`, a file-scope device array of kScratchElems int32
+// (2 MiB) that every GPU the library runs on holds until the process ends,
+// so a caller that cannot allocate (graph capture, a serving loop, a
+// harness that forbids hipMalloc) passes only inputs and outputs.
+//
+// The host never names `scratch` itself (its host-side symbol is not a
+// device address): on the first call on a device, with that device
+// current, hipGetSymbolAddress gives that device's copy, and the pointer is
+// kept per device and passed to the kernels.
+//
+// Nothing in it has to start at zero: the count kernel writes every entry
+// of the chunks it covers before the offsets kernel reads it. Calls that
+// overlap on one GPU (two streams, or a graph replay beside an eager call)
+// share the array and race.
+
+namespace sb {
+namespace {
+
+constexpr int64_t kScratchElems = int64_t{1} << 19;
+
+__device__ __attribute__((aligned(256))) int32_t scratch[kScratchElems];
+
+int scratch_on_current_device(int32_t** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static int32_t* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(SB_ERR_HIP, "routing_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(SB_ERR_HIP, "routing_noalloc: hipGetSymbolAddress of the scratch array failed: %s",
+                  hipGetErrorString(e));
+    ptrs[dev] = static_cast<int32_t*>(p);
+  }
+  *out = ptrs[dev];
+  return SB_OK;
+}
+
+}  // namespace
+}  // namespace sb
+
+extern "C" int sb_routing_noalloc(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, int32_t k,
+                                  int32_t num_experts, int32_t ffn_dim, int32_t block_size,
+                                  const int32_t* valid_tokens, int32_t* tokens_per_expert, int32_t* padded_offsets,
+                                  int32_t* row_token, int32_t* copy_row, int32_t* row_block_expert,
+                                  int32_t* row_offsets, int32_t* col_indices, int32_t* error, void* stream) {
+  if (num_tokens <= 0 || k <= 0) return fail(SB_ERR_INVALID, "expert_idx must be [T, k] with T, k > 0");
+  int64_t max_row_blocks = 0, max_rows = 0, ws = 0;
+  if (int rc = sb_routing_sizes(num_tokens * k, num_experts, ffn_dim, block_size, &max_row_blocks, &max_rows, &ws))
+    return rc;
+  if (ws > kScratchElems)
+    return fail(SB_ERR_INVALID,
+                "routing_noalloc: %lld copies over %d experts need %lld int32 of scratch, more than the %lld of "
+                "the fixed array (use sb_routing with a workspace)",
+                static_cast<long long>(num_tokens * k), num_experts, static_cast<long long>(ws),
+                static_cast<long long>(kScratchElems));
+  int32_t* ws_ptr = nullptr;
+  if (int rc = scratch_on_current_device(&ws_ptr)) return rc;
+  return sb_routing(expert_idx, idx_is_i64, num_tokens, k, num_experts, ffn_dim, block_size, valid_tokens, ws_ptr,
+                    tokens_per_expert, padded_offsets, row_token, copy_row, row_block_expert, row_offsets,
+                    col_indices, error, stream);
 }

@@ -18,7 +18,9 @@ Also reported (same JSON line): eager-mode layer time, per-stage times from
 events at the layer's stage marks (each of SDD and DSD is exactly one kernel,
 so its stage time is that kernel's duration on its stream), the roofline of
 the dominant kernel, and the CPU baseline: the oracle's fp32 loop-over-experts
-layer on this host's cores, timed on a bounded sample.
+layer on this host's cores, on the benchmark's CPU configuration (T=256,
+D=128, F=512, E=8) with os.cpu_count() threads and with 1 thread, plus the
+GPU workload itself in fp32 for scale.
 
 Before timing, the layer's output is checked against a plain-torch fp32
 reference on the GPU (max |err| / max |ref| <= 2e-2); a wrong layer is not timed.
@@ -97,43 +99,88 @@ def measured_traffic(config: str, routing: str, stage: str) -> int | None:
     return None
 
 
-def cpu_baseline(shape, routing: str, seed: int) -> dict:
-    """The oracle's fp32 layer on the host cores, on a bounded sample of the workload.
-
-    Sample: the whole layer (every expert, every token), repeated until about
-    10 s of CPU work is done (at least 3 runs, at most 200); the median run
-    is scaled to useful TFLOP/s.
-    """
+def _time_cpu_layer(x, idx, gates, w1, w2, threads: int, warmup: int, runs: int, budget_s: float | None = None
+                    ) -> list[float]:
+    """Seconds per run of the oracle's fp32 loop-over-experts layer with `threads` torch threads."""
     from oracle.moe_ref import moe_reference  # CPU baseline leg only
-    from sparsebench_amd.workloads import make_layer
 
-    threads = torch.get_num_threads()
-    x, idx, gates, w1, w2 = make_layer(shape, routing, seed, device="cpu", dtype=torch.float32)
-    copies = int(idx.numel())
-    moe_reference(x[:64], idx[:64], gates[:64], w1, w2)  # warm up
-    times = []
-    budget_s = 10.0
-    start_all = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - start_all < budget_s and len(times) < 200):
-        t0 = time.perf_counter()
-        moe_reference(x, idx, gates, w1, w2)
-        times.append(time.perf_counter() - t0)
-    flops = 2 * 2 * copies * shape.d_model * shape.ffn_dim
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        for _ in range(warmup):
+            moe_reference(x, idx, gates, w1, w2)
+        times: list[float] = []
+        start = time.perf_counter()
+        while len(times) < runs or (budget_s is not None and time.perf_counter() - start < budget_s
+                                     and len(times) < 200):
+            t0 = time.perf_counter()
+            moe_reference(x, idx, gates, w1, w2)
+            times.append(time.perf_counter() - t0)
+        return times
+    finally:
+        torch.set_num_threads(saved)
+
+
+def cpu_baseline(shape, routing: str, seed: int) -> dict:
+    """The oracle's fp32 loop-over-experts layer (the algorithm of the
+    reference's sparsebench/reference.py:49-61) on this host's cores.
+
+    value: configuration 1 of the benchmark (T=256, D=128, F=512, E=8, top-2,
+    seed 0), 3 warm-ups then the median of 20 runs, with os.cpu_count()
+    threads; also with 1 thread. Extra: the benchmarked GPU workload itself
+    in fp32 with torch's default thread count, repeated for about 10 s of
+    CPU work (at least 3 runs), for scale.
+    """
+    from sparsebench_amd.workloads import SHAPES, make_layer
+
+    cores = os.cpu_count() or 1
+    small = SHAPES["cpu_reference"]
+    x, idx, gates, w1, w2 = make_layer(small, "random", 0, device="cpu", dtype=torch.float32)
+    small_flops = small.useful_flops
+
+    def leg(threads: int) -> dict:
+        sec = statistics.median(_time_cpu_layer(x, idx, gates, w1, w2, threads, warmup=3, runs=20))
+        return {"value": round(small_flops / sec / 1e12, 6), "ms_per_sample": round(sec * 1e3, 4), "threads": threads}
+
+    all_cores, one_core = leg(cores), leg(1)
+
+    default_threads = torch.get_num_threads()
+    bx, bidx, bgates, bw1, bw2 = make_layer(shape, routing, seed, device="cpu", dtype=torch.float32)
+    times = _time_cpu_layer(bx, bidx, bgates, bw1, bw2, default_threads, warmup=1, runs=3, budget_s=10.0)
     sec = statistics.median(times)
     return {
-        "value": round(flops / sec / 1e12, 6),
+        "value": all_cores["value"],
         "unit": "TFLOP/s",
-        "cores": threads,
+        "cores": cores,
         "kind": "port",
-        "sample": (f"oracle fp32 loop-over-experts layer (oracle/moe_ref.py) on the whole {shape.name} layer, "
-                   f"{routing} routing ({copies} copies), median of {len(times)} runs over "
-                   f"{sum(times):.1f} s, {sec * 1e3:.1f} ms each, torch CPU with {threads} threads"),
-        "ms_per_sample": round(sec * 1e3, 3),
+        "sample": (f"benchmark configuration 1 (T={small.num_tokens}, D={small.d_model}, F={small.ffn_dim}, "
+                   f"E={small.num_experts}, top-2, seed 0): oracle fp32 loop-over-experts layer "
+                   f"(oracle/moe_ref.py), 3 warm-ups, median of 20 runs, torch CPU with os.cpu_count() = "
+                   f"{cores} threads"),
+        "ms_per_sample": all_cores["ms_per_sample"],
+        "single_thread": one_core,
         "cpu_model": _cpu_model(),
+        "os_cpu_count": cores,
+        "gpu_workload_fp32": {
+            "value": round(shape.useful_flops / sec / 1e12, 6), "unit": "TFLOP/s", "threads": default_threads,
+            "ms_per_sample": round(sec * 1e3, 3),
+            "sample": (f"the whole {shape.name} layer in fp32, {routing} routing, median of {len(times)} runs "
+                       f"over {sum(times):.1f} s"),
+        },
     }
 
 
 def _cpu_model() -> str:
+    """Model name as lscpu prints it (from /proc/cpuinfo when lscpu is absent)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -277,7 +324,8 @@ def main() -> int:
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline ...", flush=True)
         cpu = cpu_baseline(shape, args.routing, args.seed)
-        print(f"[bench] CPU baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads", flush=True)
+        print(f"[bench] CPU baseline (config 1): {cpu['value']} TFLOP/s on {cpu['cores']} threads, "
+              f"{cpu['single_thread']['value']} on 1 thread; {cpu['cpu_model']}", flush=True)
 
     if args.kernel_loop:
         with torch.cuda.stream(stream):
@@ -287,7 +335,8 @@ def main() -> int:
 
     tflops = shape.useful_flops / (ms * 1e-3) / 1e12
     line = {
-        "metric": "MoE fwd layer ms + useful TFLOP/s, D1024 F4096 E64, 4096 tok top-2 bf16",
+        "metric": (f"MoE fwd layer ms + useful TFLOP/s, D{shape.d_model} F{shape.ffn_dim} E{shape.num_experts}, "
+                   f"{shape.num_tokens} tok top-{shape.top_k} bf16"),
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,

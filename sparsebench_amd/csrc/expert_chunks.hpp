@@ -126,10 +126,14 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
 //             blocks per expert the row-block tiles are faster). The SDD's
 //             expert tiles leave padding rows past each expert's last
 //             32-row group unwritten, so they must only feed the DSD's
-//             expert tiles, which do not read them: kGateSdd implies
-//             kGateDsd. (A row-block DSD would read those rows, cold from
-//             HBM rather than from the cache the SDD's stores warm: with
-//             skewed routing that costs it more than the SDD gains.)
+//             expert tiles, which do not read them: the SDD takes its
+//             expert tiles only when the DSD will take its own (kGateDsd,
+//             and the DSD's grid holds all of its expert tiles; both
+//             kernels compute that from the same counts and the same grid
+//             size). A row-block DSD would read those rows, cold from HBM
+//             rather than from the cache the SDD's stores warm (with skewed
+//             routing that costs it more than the SDD gains), and write
+//             their unspecified products to padding rows of its output.
 enum ExpertGate : int32_t { kGateNone = 0, kGateDsd = 1, kGateSdd = 2 };
 
 // What a workgroup needs to choose and to number its tiles, from one pass
@@ -139,13 +143,14 @@ struct LayoutSummary {
   int32_t largest;   // real rows of the largest expert
   int32_t chunks_a;  // chunks of up to 32 RA rows
   int32_t chunks_b;  // chunks of up to 32 RB rows
+  int32_t chunks_c;  // chunks of up to 32 RC rows (0 when RC is 0)
 };
 
-template <int RA, int RB>
+template <int RA, int RB, int RC = 0>
 __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restrict__ tokens_per_expert,
                                                           int32_t num_experts) {
   int64_t rows = 0;
-  int32_t most = 0, ca = 0, cb = 0;
+  int32_t most = 0, ca = 0, cb = 0, cc = 0;
 #pragma unroll 1
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
@@ -154,6 +159,7 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
     most = max(most, v);
     ca += Chunking<RA>::count(v);
     cb += Chunking<RB>::count(v);
+    if constexpr (RC > 0) cc += Chunking<RC>::count(v);
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
@@ -161,12 +167,14 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
     most = max(most, __shfl_xor(most, d, 64));
     ca += __shfl_xor(ca, d, 64);
     cb += __shfl_xor(cb, d, 64);
+    if constexpr (RC > 0) cc += __shfl_xor(cc, d, 64);
   }
   LayoutSummary sum;
   sum.rows = rows;
   sum.largest = __builtin_amdgcn_readfirstlane(most);
   sum.chunks_a = __builtin_amdgcn_readfirstlane(ca);
   sum.chunks_b = __builtin_amdgcn_readfirstlane(cb);
+  sum.chunks_c = __builtin_amdgcn_readfirstlane(cc);
   return sum;
 }
 

@@ -150,6 +150,10 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
   });
 }
 
+// Expert tiles of the DSD (defined below): 4 waves, 256 columns, chunks of up
+// to 256 rows. The SDD's choice follows the DSD's, so both are needed here.
+constexpr int kDsdBN = 256, kDsdWaves = 4, kDsdRmax = 8, kDsdStages = 4;
+
 // Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 192 rows;
 // tiles of up to 128 rows have a 4-stage ring (4 x 40 KB fits the 160 KB).
 constexpr int kSddBN = 512, kSddWaves = 8, kSddRmax = 6, kSddStages = 3;
@@ -161,7 +165,7 @@ __global__ void __launch_bounds__(64 * kSddWaves)
                      const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ tokens_per_expert,
                      const int32_t* __restrict__ padded_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
                      int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t max_row_blocks,
-                     int32_t apply_gelu, int32_t group, int32_t force) {
+                     int32_t apply_gelu, int32_t group, int32_t force, int32_t dsd_grid) {
   static_assert(CfgB::kThreads == 64 * kSddWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
   __shared__ __attribute__((aligned(1024)))
   uint8_t lds[max_int(max_int(chunk_lds_bytes<kSddBN, kSddWaves, kSddStages, kSddRmax>(),
@@ -172,9 +176,13 @@ __global__ void __launch_bounds__(64 * kSddWaves)
   // blocks x slices tiles either way.
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   if (static_cast<int>(blockIdx.x) >= live_rb * (ffn_dim / kSddBN)) return;
-  const LayoutSummary sum = summarize_layout<kSddRmax, 4>(tokens_per_expert, num_experts);
+  const LayoutSummary sum = summarize_layout<kSddRmax, 4, kDsdRmax>(tokens_per_expert, num_experts);
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
-  if (!expert_stage_runs(sum, num_experts, kGateSdd, force)) {
+  // The DSD's own choice (dsd_layer_kernel): its expert tiles when the
+  // routing is balanced and its grid of dsd_grid workgroups holds them all.
+  const bool dsd_expert = force == 1 || (expert_stage_runs(sum, num_experts, kGateDsd, force) &&
+                                         static_cast<int64_t>(sum.chunks_c) * (d_model / kDsdBN) <= dsd_grid);
+  if (!(expert_stage_runs(sum, num_experts, kGateSdd, force) && dsd_expert)) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in
     // order; every row is computed and written (padding rows read as zeros).
     const int blocks = sum.chunks_b;
@@ -279,7 +287,6 @@ __device__ __forceinline__ void dsd_chunk_tile(uint8_t* __restrict__ lds, const 
 // and written, as sb_dsd's default tile does; they run on the same tile
 // code as the expert chunks (one H buffer, K steps through the row block's
 // own F/128 blocks, as the routing layout stores them).
-constexpr int kDsdBN = 256, kDsdWaves = 4, kDsdRmax = 8, kDsdStages = 4;
 
 template <class CfgB>
 __global__ void __launch_bounds__(64 * kDsdWaves)
@@ -331,37 +338,6 @@ __global__ void __launch_bounds__(64 * kDsdWaves)
 
 // --------------------------------------------------------------- launch ---
 
-template <class CfgB>
-int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
-                     const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
-                     void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
-                     int64_t max_row_blocks, int32_t apply_gelu, int32_t force, hipStream_t stream) {
-  // Both tilings have at most max_row_blocks x F/512 tiles (every chunk
-  // starts a row block of its own).
-  static_assert(CfgB::BN == kSddBN, "one grid for both tilings");
-  const int64_t tiles = max_row_blocks * (ffn_dim / kSddBN);
-  sdd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kSddWaves, 0, stream>>>(
-      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
-      tokens_per_expert, padded_offsets, static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens),
-      static_cast<int32_t>(d_model), static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts),
-      static_cast<int32_t>(max_row_blocks), apply_gelu, kTileGroup, force);
-  return check_launch("sdd_experts");
-}
-
-int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
-                       const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
-                       void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
-                       int64_t max_row_blocks, int32_t apply_gelu, int32_t force, hipStream_t stream) {
-  // The row-block tile is sb_sdd's for the shape (sdd_tile_for).
-  if (sdd_tile_for(d_model, ffn_dim) == SddTile::kDeep)
-    return launch_sdd_layer<SddDeepTile>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
-                                         padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
-                                         max_row_blocks, apply_gelu, force, stream);
-  return launch_sdd_layer<SddWideTile>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
-                                       padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts, max_row_blocks,
-                                       apply_gelu, force, stream);
-}
-
 // CUs of the current device, read once per device.
 int device_cus(int* cus_out) {
   constexpr int kMaxDevices = 64;
@@ -379,24 +355,72 @@ int device_cus(int* cus_out) {
   return SB_OK;
 }
 
+// Workgroups of dsd_layer_kernel: every row-block tile (the 512- or
+// 256-wide tile of sb_dsd's default shape), or every expert tile up to four
+// per CU if they can be more, and no more: workgroups past the chosen
+// tiling's tiles still read the counts before they return. Expert e's
+// ceil(n_e / 256) chunks are at most 1 + (n_e - 1) / 256, so there are at
+// most min(E, N) + N / 256 of them for N routed rows, and N is at most
+// 128 max_row_blocks - 127 E + 127 (max_row_blocks = floor((N + 127 E) /
+// 128)). Expert tiles the grid cannot hold leave the stage to the row
+// blocks (on the device). A function of the layout's sizes only, so the
+// SDD's launch computes the same number for its own choice.
+int dsd_layer_grid(int64_t max_row_blocks, int64_t num_experts, int64_t d_model, int32_t force, int64_t* grid) {
+  int cus = 0;
+  if (const int rc = device_cus(&cus)) return rc;
+  const int64_t rows = std::min(max_row_blocks * kBS, std::max<int64_t>(0, max_row_blocks * kBS - (kBS - 1) * num_experts) +
+                                                          (kBS - 1));
+  const int64_t chunk_bound = std::min(max_row_blocks, std::min(num_experts, rows) + rows / (32 * kDsdRmax));
+  const int64_t expert_tiles = chunk_bound * (d_model / kDsdBN);
+  const int64_t forced_expert = force == 1 ? expert_tiles : 0;
+  const int64_t rb_bn = d_model % 512 == 0 ? 512 : 256;
+  *grid = std::max({std::min<int64_t>(expert_tiles, 4 * static_cast<int64_t>(cus)), forced_expert,
+                    max_row_blocks * (d_model / rb_bn)});
+  return SB_OK;
+}
+
+template <class CfgB>
+int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+                     const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
+                     void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
+                     int64_t max_row_blocks, int32_t apply_gelu, int32_t force, hipStream_t stream) {
+  // Both tilings have at most max_row_blocks x F/512 tiles (every chunk
+  // starts a row block of its own).
+  static_assert(CfgB::BN == kSddBN, "one grid for both tilings");
+  const int64_t tiles = max_row_blocks * (ffn_dim / kSddBN);
+  int64_t dsd_grid = 0;  // no DSD expert tiles for D % 256 != 0
+  if (d_model % kDsdBN == 0)
+    if (const int rc = dsd_layer_grid(max_row_blocks, num_experts, d_model, force, &dsd_grid)) return rc;
+  sdd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kSddWaves, 0, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
+      tokens_per_expert, padded_offsets, static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens),
+      static_cast<int32_t>(d_model), static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts),
+      static_cast<int32_t>(max_row_blocks), apply_gelu, kTileGroup, force,
+      static_cast<int32_t>(std::min<int64_t>(dsd_grid, 2147483647)));
+  return check_launch("sdd_experts");
+}
+
+int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
+                       const int32_t* row_offsets, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
+                       void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim, int64_t num_experts,
+                       int64_t max_row_blocks, int32_t apply_gelu, int32_t force, hipStream_t stream) {
+  // The row-block tile is sb_sdd's for the shape (sdd_tile_for).
+  if (sdd_tile_for(d_model, ffn_dim) == SddTile::kDeep)
+    return launch_sdd_layer<SddDeepTile>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
+                                         padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
+                                         max_row_blocks, apply_gelu, force, stream);
+  return launch_sdd_layer<SddWideTile>(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert,
+                                       padded_offsets, out, num_tokens, d_model, ffn_dim, num_experts, max_row_blocks,
+                                       apply_gelu, force, stream);
+}
+
 template <class CfgB>
 int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
                      const int32_t* row_block_expert, void* out, int64_t max_row_blocks, int64_t num_experts,
                      int64_t num_copies, int64_t ffn_dim, int64_t d_model, int32_t force, hipStream_t stream) {
-  // Workgroups: every row-block tile, or every expert tile up to four per
-  // CU if they can be more, and no more: workgroups past the chosen
-  // tiling's tiles still read the counts before they return. Expert e's
-  // ceil(n_e / 256) chunks are at most 1 + (n_e - 1) / 256, so there are at
-  // most min(E, N) + N / 256 of them for N routed rows. Expert tiles the
-  // grid cannot hold would leave the rest to the row blocks (on the device).
-  int cus = 0;
-  if (const int rc = device_cus(&cus)) return rc;
-  const int64_t rows = std::min(num_copies, max_row_blocks * kBS);
-  const int64_t chunk_bound = std::min(max_row_blocks, std::min(num_experts, rows) + rows / (32 * kDsdRmax));
-  const int64_t expert_tiles = chunk_bound * (d_model / kDsdBN);
-  const int64_t forced_expert = expert_gate_override() == 1 ? expert_tiles : 0;
-  const int64_t tiles = std::max({std::min<int64_t>(expert_tiles, 4 * static_cast<int64_t>(cus)), forced_expert,
-                                  max_row_blocks * (d_model / CfgB::BN)});
+  static_assert(CfgB::BN == 512 || CfgB::BN == 256, "row-block tile widths of dsd_layer_grid");
+  int64_t tiles = 0;
+  if (const int rc = dsd_layer_grid(max_row_blocks, num_experts, d_model, force, &tiles)) return rc;
   const int64_t h_bytes = max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2;
   dsd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kDsdWaves, 0, stream>>>(
       static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w2), tokens_per_expert, padded_offsets,

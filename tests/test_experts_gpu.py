@@ -246,14 +246,28 @@ def test_expert_kernels_reject_bad_shapes() -> None:
                             w2.cuda().view(e * f, d), topo)
 
 
-def gate_rule(counts: list[int], stage: str) -> bool:
-    """The choice stated in expert_chunks.hpp, restated: expert tiles iff no
-    expert holds more than twice the mean rows (and, for SDD, the mean is at
-    most 256 rows)."""
+def dsd_grid(max_rb: int, e: int, d: int) -> int:
+    """Workgroups of the DSD layer kernel (dsd_layer_grid in experts.hip), restated for 256 CUs."""
+    rows = min(max_rb * 128, max(0, max_rb * 128 - 127 * e) + 127)
+    chunk_bound = min(max_rb, min(e, rows) + rows // 256)
+    return max(min(chunk_bound * (d // 256), 4 * 256), max_rb * (d // (512 if d % 512 == 0 else 256)))
+
+
+def dsd_chunks(counts: list[int]) -> int:
+    """Chunks of up to 256 rows (the DSD's expert tiles)."""
+    return sum(-(-c // 256) for c in counts if c > 0)
+
+
+def gate_rule(counts: list[int], stage: str, max_rb: int, d: int) -> bool:
+    """The choice stated in expert_chunks.hpp, restated: the DSD takes expert
+    tiles iff no expert holds more than twice the mean rows and its grid
+    holds all of them; the SDD iff, besides, the mean is at most 256 rows
+    and the DSD takes its expert tiles."""
     counts = [max(c, 0) for c in counts]
     total, most, e = sum(counts), max(counts), len(counts)
     balanced = total > 0 and most * e <= 2 * total
-    return balanced and (stage == "dsd" or total <= 256 * e)
+    dsd = balanced and dsd_chunks(counts) * (d // 256) <= dsd_grid(max_rb, e, d)
+    return dsd and (stage == "dsd" or total <= 256 * e)
 
 
 @pytest.mark.parametrize("case", list(CASES))
@@ -292,7 +306,47 @@ def test_device_choice_follows_the_rule(case: str) -> None:
     dense = dense_rows(h, fb)
     if f % 512 == 0 and untouched:
         sdd_expert = bool(torch.isnan(dense[torch.tensor(untouched, device="cuda")]).all())
-        assert sdd_expert == gate_rule(counts, "sdd")
+        assert sdd_expert == gate_rule(counts, "sdd", max_rb, d)
     if pad:
         dsd_expert = bool(torch.isnan(y[torch.tensor(pad, device="cuda")]).all())
-        assert dsd_expert == gate_rule(counts, "dsd")
+        assert dsd_expert == gate_rule(counts, "dsd", max_rb, d)
+
+
+def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(monkeypatch) -> None:
+    # 130 experts with 2 rows each (balanced), D = 2048: the DSD's 130 x 8
+    # expert tiles exceed its grid (1024 workgroups on 256 CUs), so it runs
+    # row blocks, and the SDD must then run row blocks too, writing every
+    # padding row of H that the row-block DSD reads (checked from a NaN-filled
+    # H and y). The layer stays bit-identical to the per-row-block kernels.
+    from sparsebench_amd._lib import check, lib, stream_of
+    from sparsebench_amd.moe import moe_forward
+    from sparsebench_amd.routing import route_device
+
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the grid bound is stated for 256 CUs")
+    e, d, f, t = 130, 2048, 512, 260
+    g = torch.Generator(device="cuda").manual_seed(3)
+    idx = (torch.arange(t, device="cuda") % e).reshape(-1, 1)
+    x = torch.randn(t, d, generator=g, device="cuda").bfloat16()
+    w1 = (torch.randn(e, d, f, generator=g, device="cuda") / d**0.5).bfloat16()
+    w2 = (torch.randn(e, f, d, generator=g, device="cuda") / f**0.5).bfloat16()
+    topo = route_device(idx, e, f, 128)
+    max_rb = topo.row_token.numel() // 128
+    counts = topo.tokens_per_expert.cpu().tolist()
+    assert dsd_chunks(counts) * (d // 256) > dsd_grid(max_rb, e, d)
+    assert not gate_rule(counts, "sdd", max_rb, d) and not gate_rule(counts, "dsd", max_rb, d)
+    monkeypatch.delenv("SPARSEBENCH_EXPERT_GATE", raising=False)
+    fb = f // 128
+    h = torch.full((max_rb * fb, 128, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    check(lib().sb_sdd_experts(
+        x.data_ptr(), w1.data_ptr(), topo.row_token.data_ptr(), topo.row_block_expert.data_ptr(),
+        topo.row_offsets.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
+        h.data_ptr(), t, d, f, e, max_rb, 1, stream_of(x.device)))
+    torch.cuda.synchronize()
+    live = int(topo.padded_offsets[-1])
+    assert not torch.isnan(dense_rows(h, fb)[:live]).any(), "every row of every live row block is written"
+    gates = torch.ones(t, 1, device="cuda")
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    ref = moe_forward(x, idx, gates, w1, w2)
+    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
+    assert torch.equal(moe_forward(x, idx, gates, w1, w2), ref)

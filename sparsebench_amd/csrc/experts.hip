@@ -507,7 +507,7 @@ extern "C" int sb_dsd_experts(const void* h, const void* w2, const int32_t* toke
     return sb_dsd(h, w2, row_offsets, col_indices, out, max_row_blocks * (ffn_dim / kBS), num_experts * ffn_dim,
                   max_row_blocks, kBS, d_model, 0, stream);
   const hipStream_t s = as_stream(stream);
-  // Row-block tile: sb_dsd's default 128 x 512 tile of 4 waves (v64);
+  // Row-block tile: sb_dsd's 128 x 512 tile of 4 waves (its tile for K < 8192);
   // 128 x 256 when D % 512 != 0.
   const int rc = d_model % 512 == 0
                      ? launch_dsd_layer<ChunkCfg<4, 512, 4, 4>>(h, w2, tokens_per_expert, padded_offsets,

@@ -1,8 +1,8 @@
 """The SDD / DSD stages of moe_forward (sb_sdd_experts, sb_dsd_experts)
 against the per-row-block kernels and the oracle.
 
-Each entry point launches an expert-major kernel and the per-row-block
-kernel; on the GPU one of them does the work (the expert tiles when the
+Each entry point launches one kernel whose workgroups choose, on the GPU,
+between expert-chunk tiles and row-block tiles (the expert tiles when the
 routing is balanced). SPARSEBENCH_EXPERT_GATE=1 / 2 forces one side, so
 both are tested on every routing here, and 0 (unset) tests the choice.
 
@@ -11,7 +11,7 @@ dsd_cuda write for it: both accumulate each output in fp32 over K in the same
 order of 16-deep MFMA steps, and a row's result depends on that row alone.
 SDD's padding rows up to the chunk's next multiple of 32 are zeros. The
 per-row-block kernels are themselves pinned to the oracle (test_sdd_gpu.py,
-test_dsd_gpu.py); one oracle check per variant is repeated here.
+test_dsd_gpu.py); one oracle check per tiling is repeated here.
 
 The routings put experts on every side of the chunking's edges: 0, 1, 31,
 32, 33, 127, 128, 129, 160, 161, 192 (one 192-row SDD tile), 193 (two), 255,

@@ -6,16 +6,20 @@
 // layout of sparsebench/topology.py:53-118 (reference), bit for bit, with the
 // worst-case buffer conventions of csrc/routing.cu:162-193, 248-249.
 //
-// Three launches, all on the caller's stream:
+// Launches, all on the caller's stream:
 //   1. count    one workgroup per chunk of 1024 copies: per-expert counts of
 //               the chunk, plus a count of bad ids in column E.
-//   2. offsets  one workgroup: exclusive prefix of every expert's column over
-//               the chunks (in place), tokens_per_expert, padded_offsets, error.
+//   2. offsets  (only beyond kScanChunks chunks) one workgroup: exclusive
+//               prefix of every expert's column over the chunks (in place),
+//               tokens_per_expert, padded_offsets, error.
 //   3. place    first C workgroups: each copy's row, ranked inside its wave
 //               by ballot bit-slicing (no atomics, so the order is stable);
 //               the remaining workgroups write row_offsets / col_indices /
-//               row_block_expert and mark every non-copy row -1.
-// Place's two roles touch disjoint memory and depend only on step 2.
+//               row_block_expert and mark every non-copy row -1. Up to
+//               kScanChunks chunks, every workgroup first sums the columns
+//               of the counts itself (route_place_scan_kernel), in place of
+//               step 2.
+// Place's two roles touch disjoint memory and depend only on steps 1-2.
 
 #include <mutex>
 
@@ -232,6 +236,98 @@ __global__ void __launch_bounds__(kChunk)
               row_block_expert, row_offsets, col_indices);
 }
 
+// Place and layout for at most kScanChunks chunks, straight from the count
+// kernel's per-chunk counts: each workgroup sums every expert's column
+// itself (one lane per expert; num_chunks loads each), over the chunks
+// before its own and over all of them, and scans the padded sizes in LDS.
+// That replaces the one-workgroup offsets kernel and its launch. Workgroup 0
+// also writes tokens_per_expert, padded_offsets and the error flag. The
+// rest is route_place_kernel's placement and layout.
+constexpr int kScanChunks = 32;
+
+template <typename Idx, typename Tok>
+__global__ void __launch_bounds__(kChunk)
+    route_place_scan_kernel(const Idx* __restrict__ idx, int64_t n, TokenSource<Tok> tokens, int32_t num_experts,
+                            int32_t num_bits, const int32_t* __restrict__ valid_tokens, int32_t num_chunks,
+                            const int32_t* __restrict__ counts, int32_t block_size, int32_t ffn_blocks,
+                            int32_t max_row_blocks, int64_t max_rows, int32_t* __restrict__ tokens_per_expert,
+                            int32_t* __restrict__ padded_offsets, int32_t* __restrict__ error,
+                            int32_t* __restrict__ copy_row, int32_t* __restrict__ row_token,
+                            int32_t* __restrict__ row_block_expert, int32_t* __restrict__ row_offsets,
+                            int32_t* __restrict__ col_indices) {
+  __shared__ int32_t total[kMaxExperts];   // copies of each expert in all chunks
+  __shared__ int32_t before[kMaxExperts];  // copies of each expert in the chunks before this one
+  __shared__ int32_t offs[kMaxExperts + 1];
+  __shared__ int32_t wave_counts[kWaves * kMaxExperts];
+  __shared__ int64_t wave_sums[kWaves];
+  const int tid = threadIdx.x;
+  const bool placing = static_cast<int32_t>(blockIdx.x) < num_chunks;
+  const int own = placing ? static_cast<int>(blockIdx.x) : num_chunks;
+  const int64_t stride = num_experts + 1;
+
+  // Column tid (expert tid): all of its at most kScanChunks loads are issued
+  // before the first is used, so they are in flight together.
+  int32_t sum_before = 0, sum_all = 0;
+  if (tid < num_experts) {
+    int32_t v[kScanChunks];
+#pragma unroll
+    for (int b = 0; b < kScanChunks; ++b) v[b] = b < num_chunks ? counts[b * stride + tid] : 0;
+#pragma unroll
+    for (int b = 0; b < kScanChunks; ++b) {
+      sum_before += b < own ? v[b] : 0;
+      sum_all += v[b];
+    }
+    total[tid] = sum_all;
+    before[tid] = sum_before;
+  }
+  const int64_t padded =
+      tid < num_experts ? (static_cast<int64_t>(sum_all) + block_size - 1) / block_size * block_size : 0;
+  const int64_t incl = block_inclusive_scan(padded, wave_sums);  // synchronizes the workgroup
+  if (tid < num_experts) offs[tid + 1] = static_cast<int32_t>(incl);
+  if (tid == 0) offs[0] = 0;
+  if (blockIdx.x == 0) {
+    if (tid < num_experts) {
+      tokens_per_expert[tid] = sum_all;
+      padded_offsets[tid + 1] = static_cast<int32_t>(incl);
+    }
+    if (tid == 0) {
+      padded_offsets[0] = 0;
+      int32_t bad = 0;  // column E: copies with a bad id
+      for (int b = 0; b < num_chunks; ++b) bad += counts[b * stride + num_experts];
+      error[0] = bad > 0 ? 1 : 0;
+    }
+  }
+
+  if (placing) {
+    for (int i = tid; i < kWaves * num_experts; i += kChunk) wave_counts[i] = 0;
+    __syncthreads();
+    const int wave = tid >> 6;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kChunk + tid;
+    bool bad;
+    int32_t token;
+    const int32_t e = read_expert(idx, c, n, tokens, num_experts, valid_tokens, &bad, &token);
+    const bool valid = e >= 0;
+    const uint64_t peers = same_expert_lanes(valid, e, num_bits);
+    const uint64_t lower = peers & lanes_below();
+    if (valid && lower == 0) wave_counts[wave * num_experts + e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int32_t in_waves = 0;
+      for (int w = 0; w < wave; ++w) in_waves += wave_counts[w * num_experts + e];
+      const int32_t row = offs[e] + before[e] + in_waves + __popcll(lower);
+      copy_row[c] = row;
+      row_token[row] = token;
+    } else if (c < n) {
+      copy_row[c] = -1;
+    }
+    return;
+  }
+  __syncthreads();
+  const int64_t i = static_cast<int64_t>(blockIdx.x - num_chunks) * kLayoutItemsPerGroup + tid;
+  layout_item(i, offs, total, num_experts, block_size, ffn_blocks, max_row_blocks, max_rows, row_token,
+              row_block_expert, row_offsets, col_indices);
+}
+
 int bits_for(int32_t num_experts) {
   int b = 0;
   while ((1 << b) < num_experts) ++b;
@@ -268,7 +364,9 @@ extern "C" int sb_routing_sizes(int64_t num_copies, int32_t num_experts, int32_t
 namespace sb {
 namespace {
 
-// The three routing launches for n copies whose tokens come from `tokens`.
+// Routing of n copies whose tokens come from `tokens`: count, then place with
+// the offsets scan inside for at most kScanChunks chunks; count, offsets and
+// place beyond.
 template <typename Idx, typename Tok>
 int launch_routing(const Idx* idx, int64_t n, TokenSource<Tok> tokens, int32_t num_experts, int32_t ffn_dim,
                    int32_t block_size, const int32_t* valid_tokens, int32_t* workspace, int32_t* tokens_per_expert,
@@ -285,6 +383,13 @@ int launch_routing(const Idx* idx, int64_t n, TokenSource<Tok> tokens, int32_t n
   route_count_kernel<Idx, Tok><<<num_chunks, kChunk, 0, stream>>>(idx, n, tokens, num_experts, num_bits,
                                                                   valid_tokens, workspace);
   if (int rc = check_launch("routing count")) return rc;
+  if (num_chunks <= kScanChunks) {
+    route_place_scan_kernel<Idx, Tok><<<num_chunks + layout_groups, kChunk, 0, stream>>>(
+        idx, n, tokens, num_experts, num_bits, valid_tokens, num_chunks, workspace, block_size, ffn_blocks,
+        static_cast<int32_t>(max_row_blocks), max_rows, tokens_per_expert, padded_offsets, error, copy_row, row_token,
+        row_block_expert, row_offsets, col_indices);
+    return check_launch("routing place");
+  }
   route_offsets_kernel<<<1, kChunk, 0, stream>>>(workspace, num_chunks, num_experts, block_size, tokens_per_expert,
                                                  padded_offsets, error);
   if (int rc = check_launch("routing offsets")) return rc;

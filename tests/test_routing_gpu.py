@@ -60,6 +60,15 @@ def test_matches_oracle_big(case: str, num_experts: int) -> None:
     check(routing_case(case, 100_000, num_experts), num_experts, 128)
 
 
+@pytest.mark.parametrize(("case", "num_experts"), [("zipf", 128), ("random", 1024), ("skewed", 8)])
+@pytest.mark.parametrize("num_tokens", [16383, 16384, 16385])
+def test_scan_in_place_and_offsets_kernel_forms_meet(case: str, num_experts: int, num_tokens: int) -> None:
+    # Up to 32 chunks of 1024 copies, the place kernel scans the counts
+    # itself; beyond, a separate offsets kernel does: top-2 copies at 32766,
+    # 32768 and 32770 sit on both sides of the bound.
+    check(routing_case(case, num_tokens, num_experts), num_experts, 128, ffn_dim=768)
+
+
 @pytest.mark.parametrize("num_experts", [1, 3, 1023])
 def test_odd_expert_counts(num_experts: int) -> None:
     g = torch.Generator().manual_seed(11)

@@ -4,7 +4,11 @@ against sb_routing (routing with a caller-owned workspace), through the C ABI.
 Two calls in a row, the second on a smaller input, so the second call runs
 on scratch the first one left behind. Every output must be bit-identical to
 sb_routing's (integer layout work: the bar is exact), and sizes beyond the
-fixed array are rejected before anything is enqueued.
+fixed array are rejected before anything is enqueued. Up to 32768 copies
+(32 chunks of 1024) the place kernel reads the per-chunk counts straight
+from scratch; beyond, the offsets kernel scans them there in place first.
+The sizes here are on both sides of that bound, each call smaller than the
+one before.
 """
 
 import ctypes
@@ -64,15 +68,17 @@ def assert_same(a: list[torch.Tensor], b: list[torch.Tensor]) -> None:
                                                                   ("empty_middle", 8, 4)])
 def test_noalloc_matches_workspace_routing_twice(case: str, num_experts: int, block_size: int) -> None:
     ffn_dim = 4 * block_size
-    big = routing_case(case, 20000, num_experts, seed=1).cuda()
-    small = routing_case(case, 777, num_experts, seed=2).int().cuda()
-    for idx in (big, small):  # the second call is smaller: stale scratch from the first must not leak in
+    big = routing_case(case, 20000, num_experts, seed=1).cuda()  # 40000 copies: 40 chunks
+    small = routing_case(case, 17000, num_experts, seed=2).int().cuda()  # 34 chunks, over stale scratch
+    tiny = routing_case(case, 777, num_experts, seed=3).cuda()  # 2 chunks, counts scanned by the place kernel
+    for idx in (big, small, tiny):  # each call smaller: stale scratch from the one before must not leak in
         assert_same(run_noalloc(idx, num_experts, ffn_dim, block_size),
                     run_with_workspace(idx, num_experts, ffn_dim, block_size))
 
 
-def test_noalloc_bad_ids_and_valid_tokens() -> None:
-    idx = routing_case("random", 3000, 32, seed=3).cuda()
+@pytest.mark.parametrize("num_tokens", [3000, 20000])
+def test_noalloc_bad_ids_and_valid_tokens(num_tokens: int) -> None:
+    idx = routing_case("random", num_tokens, 32, seed=3).cuda()
     idx[5, 1] = 32
     idx[17, 0] = -1
     valid = torch.tensor([2500], dtype=torch.int32, device="cuda")
@@ -95,10 +101,11 @@ def test_noalloc_rejects_more_scratch_than_the_array() -> None:
     assert int(outs[0][0]) == -7  # nothing ran
 
 
-def test_noalloc_under_graph_capture() -> None:
+@pytest.mark.parametrize("num_tokens", [4096, 17000])
+def test_noalloc_under_graph_capture(num_tokens: int) -> None:
     # Captured after a first eager call on the device; every replay, with fresh
     # routing written in place between them, equals the workspace routing.
-    idx = routing_case("zipf", 4096, 64, seed=4).cuda()
+    idx = routing_case("zipf", num_tokens, 64, seed=4).cuda()
     run_noalloc(idx, 64, 512, 128)
     torch.cuda.synchronize()
     t, k = idx.shape
@@ -110,7 +117,7 @@ def test_noalloc_under_graph_capture() -> None:
                                       ctypes.c_void_p(side.cuda_stream))
     assert rc == 0
     for seed in (5, 6, 7):
-        idx.copy_(routing_case("zipf", 4096, 64, seed=seed).cuda())
+        idx.copy_(routing_case("zipf", num_tokens, 64, seed=seed).cuda())
         graph.replay()
         torch.cuda.synchronize()
         assert_same(outs, run_with_workspace(idx, 64, 512, 128))

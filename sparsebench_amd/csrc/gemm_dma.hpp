@@ -468,74 +468,6 @@ struct DmaMainloop {
     }
   }
 
-  // Persistent form: one workgroup runs a sequence of tiles, and the ring
-  // runs straight across tile boundaries. The last STAGES-1 steps of a tile
-  // issue the first steps of the next one, so its loads are in flight while
-  // this tile's epilogue runs, and no tile starts with an empty pipeline.
-  //
-  // Sched supplies
-  //   Tile                       a tile: `steps`, its number of K steps
-  //                              (may be 0), plus what its sources need
-  //   bool next(Tile&)           this workgroup's next tile; false when none
-  //   Src source(const Tile&)    the tile's step sources, as for run(), by value
-  //   void epilogue(const Tile&, Acc&)
-  // Tile metadata should be read with wave-uniform (scalar) loads: a vector
-  // load would make the compiler wait on the whole DMA queue at its use.
-  //
-  // Waits: step g's loads are done once at most the loads of the steps
-  // issued after it are outstanding. Buffer loads complete in issue order,
-  // so epilogue stores issued between them only make the wait stricter.
-  template <class Sched>
-  __device__ __forceinline__ static void run_tiles(uint8_t* lds, Sched& sched) {
-    using Tile = typename Sched::Tile;
-    Tile cur, nxt;
-    if (!sched.next(cur)) return;
-    bool has_nxt = sched.next(nxt);
-    // Issue cursor: tile slot (0 = cur, 1 = nxt) and that tile's next step.
-    int slot = 0, ik = 0;
-    int issued = 0, done = 0;  // steps issued / computed by this workgroup
-    auto issue_next = [&]() {
-      if (slot == 0 && ik >= cur.steps) {
-        if (!has_nxt) return;
-        slot = 1;
-        ik = 0;
-      }
-      if (slot == 1 && ik >= nxt.steps) return;
-      // By value: the choice is a uniform select, not a pointer into the
-      // two tiles (which would move them to scratch).
-      const auto src = slot == 0 ? sched.source(cur) : sched.source(nxt);
-      issue(lds, issued, ik, src);
-      ++ik;
-      ++issued;
-    };
-#pragma unroll
-    for (int s = 0; s < Cfg::STAGES - 1; ++s) issue_next();
-    while (true) {
-      Acc acc;
-#pragma unroll
-      for (int jn = 0; jn < Cfg::TN; ++jn)
-#pragma unroll
-        for (int i = 0; i < Cfg::TM; ++i)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[jn][i][v] = 0.0f;
-      for (int k = 0; k < cur.steps; ++k, ++done) {
-        wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(issued - done - 1);
-        __builtin_amdgcn_s_barrier();
-        issue_next();
-        compute(lds + (done % Cfg::STAGES) * Cfg::kStageBytes, acc);
-      }
-      sched.epilogue(cur, acc);
-      if (!has_nxt) break;
-      cur = nxt;
-      if (slot == 1) {
-        slot = 0;  // ik already counts the new cur's issued steps
-      } else {
-        ik = 0;  // nothing of it issued yet
-      }
-      has_nxt = sched.next(nxt);
-    }
-  }
-
   // Epilogue through LDS. A lane's results are 4 consecutive columns of 32
   // different rows, so storing them straight to memory writes each cache
   // line in 16-byte pieces. Instead the tile is written to LDS as bf16,

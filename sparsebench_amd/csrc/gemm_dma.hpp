@@ -76,36 +76,54 @@ __device__ __forceinline__ void wait_vmcnt() {
 // tiles whose accumulators leave no room for a second set).
 // EPI_PARTS: the epilogue stages the bf16 tile through LDS in this many
 // parts of BM / EPI_PARTS rows (a 192 x 512 tile does not fit at once).
+// APAIR: A is loaded two K steps at a time, as whole 128-byte rows (BK 32):
+// a 64-byte row piece costs the address and data units a whole cache line,
+// so pairing halves the A lines per byte. Stage pairs (2p, 2p+1) of the
+// ring share one A slot: [A of both | B of 2p | B of 2p+1]. The pair's A is
+// loaded with the odd step's B (one step after the even step's), when the
+// slot's previous pair has been read to the end.
 template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0, int PIPE_ = 0,
-          int EPI_PARTS_ = 1>
+          int EPI_PARTS_ = 1, int APAIR_ = 0>
 struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_;
   static constexpr int CPA = CPA_, CPB = CPB_;
   static constexpr int PIPE = PIPE_;
   static constexpr int EPI_PARTS = EPI_PARTS_;
+  static constexpr bool APAIR = APAIR_ != 0;
   static constexpr int WM = WM_, WN = WN_;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int kARowBytes = BK * 2;
-  static constexpr int kAChunksPerRow = BK / 8;
-  // DMA instructions per wave per step for A, and the A area of a stage.
-  // When BM rows do not split into whole 1 KB rows per wave, the area is
-  // rounded up: the DMA rows past BM are loaded out of range (zeros, no
-  // memory read) and never read back.
+  static constexpr int kABK = APAIR ? 2 * BK : BK;  // K width of one A slot
+  static constexpr int kARowBytes = kABK * 2;
+  static constexpr int kAChunksPerRow = kABK / 8;
+  // DMA instructions per wave for one A slot, and its area. When BM rows do
+  // not split into whole 1 KB rows per wave, the area is rounded up: the
+  // DMA rows past BM are loaded out of range (zeros, no memory read) and
+  // never read back.
   static constexpr int kAInstr = (BM * kARowBytes + 1024 * kWaves - 1) / (1024 * kWaves);
   static constexpr int kABytes = kAInstr * kWaves * 1024;
   static constexpr int kBRowBytes = BN * 2;
   static constexpr int kBBytes = BK * kBRowBytes;
   static constexpr int kStageBytes = kABytes + kBBytes;
-  static constexpr int kLdsBytes = STAGES * kStageBytes;
+  static constexpr int kPairBytes = kABytes + 2 * kBBytes;
+  static constexpr int kLdsBytes = APAIR ? (STAGES / 2) * kPairBytes : STAGES * kStageBytes;
   // LDS of a kernel: the ring, or the part of the bf16 output tile staged
   // through it in the epilogue if that is larger.
   static constexpr int kStagedPartBytes = BM * BN * 2 / EPI_PARTS;
   static constexpr int kLdsAlloc = kLdsBytes > kStagedPartBytes ? kLdsBytes : kStagedPartBytes;
   static constexpr int kBInstr = kBBytes / 1024 / kWaves;
   static constexpr int kLoadsPerStep = kAInstr + kBInstr;
+  // The wait at the top of step t, once the later steps' loads are issued:
+  // step t's loads (and, with APAIR, its pair's A) are complete once at most
+  // the loads issued after them are outstanding. Unpaired: the STAGES-2
+  // later steps'. Paired, odd t: the STAGES-2 later steps', the odd ones
+  // carrying an A pair; even t: its pair's A comes with step t+1's B, so
+  // that B and the STAGES-3 steps after it.
+  static constexpr int kLaterLoads = (STAGES - 2) * kLoadsPerStep;
+  static constexpr int kLaterLoadsOdd = (STAGES - 2) * kBInstr + (STAGES - 2) / 2 * kAInstr;
+  static constexpr int kLaterLoadsEven = (STAGES - 2) * kBInstr + (STAGES - 4) / 2 * kAInstr;
   static constexpr int kARowsPerInstr = 1024 / kARowBytes;
   static constexpr int kBRowsPerInstr = kBRowBytes >= 1024 ? 1 : 1024 / kBRowBytes;
   static_assert(kBRowBytes <= 1024, "one DMA row per instruction at most");
@@ -117,7 +135,9 @@ struct DmaCfg {
   static_assert(kBInstr >= 1 && kBInstr * kWaves * 1024 == kBBytes, "B step splits into whole 1 KB DMA rows");
   static_assert(STAGES >= 2 && STAGES <= 8, "STAGES");
   static_assert(kLdsAlloc <= 160 * 1024, "LDS");
-  static_assert(kLoadsPerStep * (STAGES - 2) <= 63, "vmcnt");
+  static_assert((APAIR ? kLaterLoadsOdd : kLaterLoads) <= 63, "vmcnt");
+  static_assert(!APAIR || (BK == 32 && STAGES % 2 == 0 && (PIPE == 3 || PIPE == 4)),
+                "paired A: BK 32, whole stage pairs, DMA among the MFMAs");
   static_assert(EPI_PARTS == 1 || (WM == 1 && TM % EPI_PARTS == 0), "epilogue parts of whole row groups");
 };
 
@@ -141,7 +161,7 @@ struct ADmaPos {
 #pragma unroll
     for (int q = 0; q < Cfg::kAInstr; ++q) {
       row[q] = Cfg::kARowsPerInstr * (Cfg::kAInstr * wave + q) + lane / Cfg::kAChunksPerRow;
-      chunk[q] = (lane % Cfg::kAChunksPerRow) ^ swz_a<Cfg::BK>(row[q]);
+      chunk[q] = (lane % Cfg::kAChunksPerRow) ^ swz_a<Cfg::kABK>(row[q]);
     }
   }
 };
@@ -226,78 +246,113 @@ template <class Cfg>
 struct DmaMainloop {
   using Acc = f32x16_t[Cfg::TN][Cfg::TM];  // acc[j][i]: C^T block (n block j, m block i)
 
-  // issue() and compute() take their LDS stage through __restrict__ pointers:
-  // the DMA of step t+STAGES-1 writes a different stage than the one step t
+  // issue() and compute() take their LDS slots through __restrict__ pointers:
+  // the DMA of step t+STAGES-1 writes different slots than the ones step t
   // reads, and saying so lets the compiler drop the vmcnt(0) it would
   // otherwise put before every LDS read (which serializes loads and MFMAs).
-  // The DMA of K step `t` of `src` into ring slot `ring % STAGES`.
-  // The DMA instructions of one K step: dma(q), q < kLoadsPerStep, issues
-  // this wave's instruction q (A rows first, then B rows).
-  template <class Src>
+  // Slots of K step t: its A (shared by a stage pair with APAIR) and its B.
+  __device__ __forceinline__ static uint8_t* a_slot(uint8_t* lds, int t) {
+    if constexpr (Cfg::APAIR) return lds + ((t >> 1) % (Cfg::STAGES / 2)) * Cfg::kPairBytes;
+    else return lds + (t % Cfg::STAGES) * Cfg::kStageBytes;
+  }
+  __device__ __forceinline__ static uint8_t* b_slot(uint8_t* lds, int t) {
+    if constexpr (Cfg::APAIR)
+      return lds + ((t >> 1) % (Cfg::STAGES / 2)) * Cfg::kPairBytes + Cfg::kABytes + (t & 1) * Cfg::kBBytes;
+    else return lds + (t % Cfg::STAGES) * Cfg::kStageBytes + Cfg::kABytes;
+  }
+
+  // The DMA instructions of K step `tb`'s B and, if kWithA, of the A slot
+  // that starts at K step `ta`: dma(q), q < kCount, issues this wave's
+  // instruction q (A rows first, then B rows). Unpaired: ta = tb. Paired:
+  // odd steps tb also load their pair's A (ta = tb - 1), even ones only B.
+  template <class Src, bool kWithA = true>
   struct StepDma {
-    uint8_t* __restrict__ stage;
+    static constexpr int kA = kWithA ? Cfg::kAInstr : 0;
+    static constexpr int kCount = kA + Cfg::kBInstr;
+    uint8_t* __restrict__ a_dst;
+    uint8_t* __restrict__ b_dst;
     __amdgpu_buffer_rsrc_t ra, rb;
     uint32_t sa, sb;
     const Src& src;
     int wave, t;
-    __device__ __forceinline__ StepDma(uint8_t* __restrict__ stage_, int t_, const Src& src_)
-        : stage(stage_), src(src_), t(t_) {
+    __device__ __forceinline__ StepDma(uint8_t* __restrict__ a_dst_, int ta, uint8_t* __restrict__ b_dst_, int tb,
+                                       const Src& src_)
+        : a_dst(a_dst_), b_dst(b_dst_), src(src_), t(ta) {
       wave = threadIdx.x >> 6;
-      src.a_src(t, &ra, &sa);
-      src.b_src(t, &rb, &sb);
+      if constexpr (kWithA) src.a_src(ta, &ra, &sa);
+      src.b_src(tb, &rb, &sb);
       // The scalar offsets are uniform by contract; saying so keeps the
       // compiler from wrapping each load in a per-lane waterfall loop when
       // it cannot prove it.
-      sa = __builtin_amdgcn_readfirstlane(sa);
+      if constexpr (kWithA) sa = __builtin_amdgcn_readfirstlane(sa);
       sb = __builtin_amdgcn_readfirstlane(sb);
     }
     __device__ __forceinline__ void operator()(int q) const {
-      if (q < Cfg::kAInstr) {
-        lds_void_t* dst = (lds_void_t*)(stage + (Cfg::kAInstr * wave + q) * 1024);
+      if (q < kA) {
+        lds_void_t* dst = (lds_void_t*)(a_dst + (Cfg::kAInstr * wave + q) * 1024);
         if constexpr (GlobalA<Src>::value)
           __builtin_amdgcn_global_load_lds(src.a_global(q, t), dst, 16, 0, Cfg::CPA);
         else
           __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst, 16, src.a_voff(q), sa, 0, Cfg::CPA);
       } else {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (lds_void_t*)(stage + Cfg::kABytes + (Cfg::kBInstr * wave + q - Cfg::kAInstr) * 1024), 16,
-            src.b_voff(q - Cfg::kAInstr), sb, 0, Cfg::CPB);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(b_dst + (Cfg::kBInstr * wave + q - kA) * 1024),
+                                                 16, src.b_voff(q - kA), sb, 0, Cfg::CPB);
       }
     }
   };
 
+  // The loads step t issues for step u = t + STAGES - 1 (or, in the
+  // prologue, for step u itself).
   template <class Src>
-  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int ring, int t, const Src& src) {
-    const StepDma<Src> dma(lds + (ring % Cfg::STAGES) * Cfg::kStageBytes, t, src);
+  __device__ __forceinline__ static StepDma<Src, true> step_dma(uint8_t* __restrict__ lds, int u, const Src& src) {
+    return StepDma<Src, true>(a_slot(lds, u), Cfg::APAIR ? u - 1 : u, b_slot(lds, u), u, src);
+  }
+  template <class Src>
+  __device__ __forceinline__ static StepDma<Src, false> step_dma_b(uint8_t* __restrict__ lds, int u, const Src& src) {
+    return StepDma<Src, false>(nullptr, 0, b_slot(lds, u), u, src);
+  }
+
+  template <class Src>
+  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int u, const Src& src) {
+    if (!Cfg::APAIR || (u & 1) != 0) {
+      const auto dma = step_dma(lds, u, src);
 #pragma unroll
-    for (int q = 0; q < Cfg::kLoadsPerStep; ++q) dma(q);
+      for (int q = 0; q < dma.kCount; ++q) dma(q);
+    } else {
+      const auto dma = step_dma_b(lds, u, src);
+#pragma unroll
+      for (int q = 0; q < dma.kCount; ++q) dma(q);
+    }
   }
 
   struct NoDma {
+    static constexpr int kCount = 0;
     __device__ __forceinline__ void operator()(int) const {}
   };
 
-  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ stage, Acc& acc) {
-    compute(stage, acc, NoDma{});
+  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ as, const uint8_t* __restrict__ bs,
+                                                 int khalf, Acc& acc) {
+    compute(as, bs, khalf, acc, NoDma{});
   }
 
-  // One K step's fragments and MFMAs. With PIPE 3, dma(q) for q <
-  // kLoadsPerStep is called among the MFMAs (a later step's loads, into
-  // another stage), spread evenly by the scheduling groups.
+  // One K step's fragments and MFMAs, from A slot `as` (K half `khalf` of
+  // it with APAIR, else 0) and B slot `bs`. With PIPE 3 and 4, dma(q) for
+  // q < Dma::kCount is called among the MFMAs (a later step's loads, into
+  // other slots), spread evenly by the scheduling groups.
   template <class Dma>
-  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ stage, Acc& acc, const Dma& dma) {
+  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ as, const uint8_t* __restrict__ bs,
+                                                 int khalf, Acc& acc, const Dma& dma) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     const int h = lane >> 5;
-    const uint8_t* as = stage;
-    const uint8_t* bs = stage + Cfg::kABytes;
+    const int kc = 4 * khalf + h;  // this lane's first 8-wide K chunk of the step in the A row
     // A side: row m = wm*WTM + 32 i + lane % 32.
     int a_row_off[Cfg::TM], a_swz[Cfg::TM];
 #pragma unroll
     for (int i = 0; i < Cfg::TM; ++i) {
       const int r = wm * Cfg::WTM + 32 * i + (lane & 31);
       a_row_off[i] = r * Cfg::kARowBytes;
-      a_swz[i] = swz_a<Cfg::BK>(r);
+      a_swz[i] = swz_a<Cfg::kABK>(r);
     }
     // W side: lane j of its 16-group reads row (k0 + j/4), columns
     // n0 + 16 (group % 2) + 4 (j % 4); chunk block (4 chunks = 64 B) of
@@ -315,7 +370,7 @@ struct DmaMainloop {
     auto read_a = [&](int s, bf16x8_t (&a)[Cfg::TM]) {
 #pragma unroll
       for (int i = 0; i < Cfg::TM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * s + h) ^ a_swz[i]) << 4));
+        a[i] = *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * s + kc) ^ a_swz[i]) << 4));
     };
     auto read_b = [&](int s, bf16x8_t (&b)[Cfg::TN]) {
 #pragma unroll
@@ -334,9 +389,9 @@ struct DmaMainloop {
           acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[jn], a[i], acc[jn][i], 0, 0, 0);
     };
     if constexpr (Cfg::PIPE == 4) {
-      constexpr int kDma = __is_same(Dma, NoDma) ? 0 : Cfg::kLoadsPerStep;
+      constexpr int kDma = Dma::kCount;
       auto read_a1 = [&](int sub, int i) {
-        return *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * sub + h) ^ a_swz[i]) << 4));
+        return *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * sub + kc) ^ a_swz[i]) << 4));
       };
       bf16x8_t a[Cfg::TM], b[2][Cfg::TN];
       read_a(0, a);
@@ -366,7 +421,7 @@ struct DmaMainloop {
       constexpr int kMfma = Cfg::TM * Cfg::TN;
       constexpr int kReads = Cfg::TM + 2 * Cfg::TN;
       constexpr int kPer = (kReads + kMfma - 1) / kMfma;
-      constexpr int kDma = __is_same(Dma, NoDma) ? 0 : Cfg::kLoadsPerStep;
+      constexpr int kDma = Dma::kCount;
       bf16x8_t a[2][Cfg::TM], b[2][Cfg::TN];
       read_a(0, a[0]);
       read_b(0, b[0]);
@@ -425,6 +480,25 @@ struct DmaMainloop {
     }
   }
 
+  // With APAIR, the wait at step t of the last STAGES-1 steps, when the
+  // `later` steps after t (all issued) are the last ones of the tile and
+  // the step count is even: odd t, those steps' B and the A pairs of the
+  // odd ones among them; even t (later is odd), its pair's A came with
+  // step t+1's B, so that B and the later-1 steps after it.
+  template <int L>
+  __device__ __forceinline__ static void wait_pair_tail(int later, bool t_odd) {
+    if constexpr (L > Cfg::STAGES - 2) {
+      wait_vmcnt<0>();
+    } else {
+      if (later == L) {
+        if (t_odd) wait_vmcnt<L * Cfg::kBInstr + (L / 2) * Cfg::kAInstr>();
+        else wait_vmcnt<L * Cfg::kBInstr + ((L > 0 ? L - 1 : 0) / 2) * Cfg::kAInstr>();
+      } else {
+        wait_pair_tail<L + 1>(later, t_odd);
+      }
+    }
+  }
+
   template <class Src>
   __device__ __forceinline__ static void run(uint8_t* lds, const Src& src, int num_steps, Acc& acc) {
 #pragma unroll
@@ -436,23 +510,42 @@ struct DmaMainloop {
     if (num_steps <= 0) return;
 #pragma unroll
     for (int s = 0; s < Cfg::STAGES - 1; ++s)
-      if (s < num_steps) issue(lds, s, s, src);
+      if (s < num_steps) issue(lds, s, src);
     if constexpr (Cfg::PIPE == 3 || Cfg::PIPE == 4) {
       // Steps that issue a later step's loads, among their MFMAs; at the top
-      // of each, steps t .. t+STAGES-2 are outstanding.
+      // of each, the loads of steps t .. t+STAGES-2 have been issued.
       int t = 0;
-      for (; t + Cfg::STAGES - 1 < num_steps; ++t) {
-        wait_vmcnt<(Cfg::STAGES - 2) * Cfg::kLoadsPerStep>();
-        __builtin_amdgcn_s_barrier();
-        const int u = t + Cfg::STAGES - 1;
-        compute(lds + (t % Cfg::STAGES) * Cfg::kStageBytes, acc,
-                StepDma<Src>(lds + (u % Cfg::STAGES) * Cfg::kStageBytes, u, src));
+      if constexpr (Cfg::APAIR) {
+        // Steps in pairs, even then odd: STAGES is even, so the even step
+        // issues an odd step's loads (B and its pair's A) and the odd step
+        // an even one's (B only).
+        for (; t + Cfg::STAGES < num_steps; t += 2) {
+          wait_vmcnt<Cfg::kLaterLoadsEven>();
+          __builtin_amdgcn_s_barrier();
+          compute(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + Cfg::STAGES - 1, src));
+          wait_vmcnt<Cfg::kLaterLoadsOdd>();
+          __builtin_amdgcn_s_barrier();
+          compute(a_slot(lds, t + 1), b_slot(lds, t + 1), 1, acc, step_dma_b(lds, t + Cfg::STAGES, src));
+        }
+        if (t + Cfg::STAGES - 1 < num_steps) {  // the last step that issues (even)
+          wait_vmcnt<Cfg::kLaterLoadsEven>();
+          __builtin_amdgcn_s_barrier();
+          compute(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + Cfg::STAGES - 1, src));
+          ++t;
+        }
+      } else {
+        for (; t + Cfg::STAGES - 1 < num_steps; ++t) {
+          wait_vmcnt<Cfg::kLaterLoads>();
+          __builtin_amdgcn_s_barrier();
+          compute(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + Cfg::STAGES - 1, src));
+        }
       }
       // The last STAGES-1 steps issue nothing.
       for (; t < num_steps; ++t) {
-        wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(num_steps - 1 - t);
+        if constexpr (Cfg::APAIR) wait_pair_tail<0>(num_steps - 1 - t, (t & 1) != 0);
+        else wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(num_steps - 1 - t);
         __builtin_amdgcn_s_barrier();
-        compute(lds + (t % Cfg::STAGES) * Cfg::kStageBytes, acc);
+        compute(a_slot(lds, t), b_slot(lds, t), Cfg::APAIR ? (t & 1) : 0, acc);
       }
       return;
     }
@@ -463,8 +556,8 @@ struct DmaMainloop {
       // Every wave's step-t data is in LDS, and every wave is done with
       // step t-1's stage, which the next issue overwrites.
       __builtin_amdgcn_s_barrier();
-      if (t + Cfg::STAGES - 1 < num_steps) issue(lds, t + Cfg::STAGES - 1, t + Cfg::STAGES - 1, src);
-      compute(lds + (t % Cfg::STAGES) * Cfg::kStageBytes, acc);
+      if (t + Cfg::STAGES - 1 < num_steps) issue(lds, t + Cfg::STAGES - 1, src);
+      compute(a_slot(lds, t), b_slot(lds, t), 0, acc);
     }
   }
 

@@ -53,10 +53,11 @@ namespace {
 // and six row groups, the 192 accumulators leave room for one set of A
 // fragments only (PIPE 4); a bf16 tile over 160 KB is staged in two parts.
 // 4-stage rings load A two K steps at a time, as whole 128-byte rows
-// (APAIR); a 3-stage ring cannot pair its stages.
+// (APAIR); in the 3-stage rings of the taller SDD tiles the extra address
+// registers would spill inside the main loop.
 template <int R, int BN, int WAVES, int STAGES>
 using ChunkCfg = DmaCfg<32 * R, BN, 32, STAGES, 1, WAVES, 0, 2, (WAVES == 8 && R >= 6) ? 4 : 3,
-                        (32 * R * BN * 2 > 160 * 1024) ? 2 : 1, STAGES % 2 == 0 ? 1 : 0>;
+                        (32 * R * BN * 2 > 160 * 1024) ? 2 : 1, STAGES == 4 ? 1 : 0>;
 
 // LDS of the expert tiles of a kernel: the largest over its tile heights.
 template <int BN, int WAVES, int STAGES, int R>

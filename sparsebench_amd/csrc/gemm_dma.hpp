@@ -78,10 +78,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 // parts of BM / EPI_PARTS rows (a 192 x 512 tile does not fit at once).
 // APAIR: A is loaded two K steps at a time, as whole 128-byte rows (BK 32):
 // a 64-byte row piece costs the address and data units a whole cache line,
-// so pairing halves the A lines per byte. Stage pairs (2p, 2p+1) of the
-// ring share one A slot: [A of both | B of 2p | B of 2p+1]. The pair's A is
-// loaded with the odd step's B (one step after the even step's), when the
-// slot's previous pair has been read to the end.
+// so pairing halves the A lines per byte. A pair m (K steps 2m, 2m+1) sits
+// in A slot m % 2, B of step t in ring slot t % STAGES (STAGES 3 or 4).
 template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0, int PIPE_ = 0,
           int EPI_PARTS_ = 1, int APAIR_ = 0>
 struct DmaCfg {
@@ -107,23 +105,20 @@ struct DmaCfg {
   static constexpr int kBRowBytes = BN * 2;
   static constexpr int kBBytes = BK * kBRowBytes;
   static constexpr int kStageBytes = kABytes + kBBytes;
-  static constexpr int kPairBytes = kABytes + 2 * kBBytes;
-  static constexpr int kLdsBytes = APAIR ? (STAGES / 2) * kPairBytes : STAGES * kStageBytes;
+  static constexpr int kLdsBytes = APAIR ? 2 * kABytes + STAGES * kBBytes : STAGES * kStageBytes;
   // LDS of a kernel: the ring, or the part of the bf16 output tile staged
   // through it in the epilogue if that is larger.
   static constexpr int kStagedPartBytes = BM * BN * 2 / EPI_PARTS;
   static constexpr int kLdsAlloc = kLdsBytes > kStagedPartBytes ? kLdsBytes : kStagedPartBytes;
   static constexpr int kBInstr = kBBytes / 1024 / kWaves;
   static constexpr int kLoadsPerStep = kAInstr + kBInstr;
-  // The wait at the top of step t, once the later steps' loads are issued:
-  // step t's loads (and, with APAIR, its pair's A) are complete once at most
-  // the loads issued after them are outstanding. Unpaired: the STAGES-2
-  // later steps'. Paired, odd t: the STAGES-2 later steps', the odd ones
-  // carrying an A pair; even t: its pair's A comes with step t+1's B, so
-  // that B and the STAGES-3 steps after it.
+  // The wait at the top of step t: step t's loads (and its A pair) are
+  // complete once at most the loads issued after them are outstanding.
+  // Unpaired: the STAGES-2 later steps'. Paired (see DmaMainloop::run):
+  // STAGES-2 steps' B, and for odd t one A pair.
   static constexpr int kLaterLoads = (STAGES - 2) * kLoadsPerStep;
-  static constexpr int kLaterLoadsOdd = (STAGES - 2) * kBInstr + (STAGES - 2) / 2 * kAInstr;
-  static constexpr int kLaterLoadsEven = (STAGES - 2) * kBInstr + (STAGES - 4) / 2 * kAInstr;
+  static constexpr int kLaterLoadsEven = (STAGES - 2) * kBInstr;
+  static constexpr int kLaterLoadsOdd = kAInstr + (STAGES - 2) * kBInstr;
   static constexpr int kARowsPerInstr = 1024 / kARowBytes;
   static constexpr int kBRowsPerInstr = kBRowBytes >= 1024 ? 1 : 1024 / kBRowBytes;
   static_assert(kBRowBytes <= 1024, "one DMA row per instruction at most");
@@ -136,8 +131,8 @@ struct DmaCfg {
   static_assert(STAGES >= 2 && STAGES <= 8, "STAGES");
   static_assert(kLdsAlloc <= 160 * 1024, "LDS");
   static_assert((APAIR ? kLaterLoadsOdd : kLaterLoads) <= 63, "vmcnt");
-  static_assert(!APAIR || (BK == 32 && STAGES % 2 == 0 && (PIPE == 3 || PIPE == 4)),
-                "paired A: BK 32, whole stage pairs, DMA among the MFMAs");
+  static_assert(!APAIR || (BK == 32 && (STAGES == 3 || STAGES == 4) && (PIPE == 3 || PIPE == 4)),
+                "paired A: BK 32, a 3- or 4-stage B ring, DMA among the MFMAs");
   static_assert(EPI_PARTS == 1 || (WM == 1 && TM % EPI_PARTS == 0), "epilogue parts of whole row groups");
 };
 
@@ -246,29 +241,27 @@ template <class Cfg>
 struct DmaMainloop {
   using Acc = f32x16_t[Cfg::TN][Cfg::TM];  // acc[j][i]: C^T block (n block j, m block i)
 
-  // issue() and compute() take their LDS slots through __restrict__ pointers:
+  // The DMA and compute() take their LDS slots through __restrict__ pointers:
   // the DMA of step t+STAGES-1 writes different slots than the ones step t
   // reads, and saying so lets the compiler drop the vmcnt(0) it would
   // otherwise put before every LDS read (which serializes loads and MFMAs).
   // Slots of K step t: its A (shared by a stage pair with APAIR) and its B.
   __device__ __forceinline__ static uint8_t* a_slot(uint8_t* lds, int t) {
-    if constexpr (Cfg::APAIR) return lds + ((t >> 1) % (Cfg::STAGES / 2)) * Cfg::kPairBytes;
+    if constexpr (Cfg::APAIR) return lds + ((t >> 1) & 1) * Cfg::kABytes;
     else return lds + (t % Cfg::STAGES) * Cfg::kStageBytes;
   }
   __device__ __forceinline__ static uint8_t* b_slot(uint8_t* lds, int t) {
-    if constexpr (Cfg::APAIR)
-      return lds + ((t >> 1) % (Cfg::STAGES / 2)) * Cfg::kPairBytes + Cfg::kABytes + (t & 1) * Cfg::kBBytes;
+    if constexpr (Cfg::APAIR) return lds + 2 * Cfg::kABytes + (t % Cfg::STAGES) * Cfg::kBBytes;
     else return lds + (t % Cfg::STAGES) * Cfg::kStageBytes + Cfg::kABytes;
   }
 
-  // The DMA instructions of K step `tb`'s B and, if kWithA, of the A slot
-  // that starts at K step `ta`: dma(q), q < kCount, issues this wave's
-  // instruction q (A rows first, then B rows). Unpaired: ta = tb. Paired:
-  // odd steps tb also load their pair's A (ta = tb - 1), even ones only B.
-  template <class Src, bool kWithA = true>
+  // The DMA instructions of the A slot that starts at K step `ta` (if
+  // kWithA) and of K step `tb`'s B (if kWithB): dma(q), q < kCount, issues
+  // this wave's instruction q (A rows first, then B rows). Unpaired: ta = tb.
+  template <class Src, bool kWithA = true, bool kWithB = true>
   struct StepDma {
     static constexpr int kA = kWithA ? Cfg::kAInstr : 0;
-    static constexpr int kCount = kA + Cfg::kBInstr;
+    static constexpr int kCount = kA + (kWithB ? Cfg::kBInstr : 0);
     uint8_t* __restrict__ a_dst;
     uint8_t* __restrict__ b_dst;
     __amdgpu_buffer_rsrc_t ra, rb;
@@ -279,13 +272,17 @@ struct DmaMainloop {
                                        const Src& src_)
         : a_dst(a_dst_), b_dst(b_dst_), src(src_), t(ta) {
       wave = threadIdx.x >> 6;
-      if constexpr (kWithA) src.a_src(ta, &ra, &sa);
-      src.b_src(tb, &rb, &sb);
       // The scalar offsets are uniform by contract; saying so keeps the
       // compiler from wrapping each load in a per-lane waterfall loop when
       // it cannot prove it.
-      if constexpr (kWithA) sa = __builtin_amdgcn_readfirstlane(sa);
-      sb = __builtin_amdgcn_readfirstlane(sb);
+      if constexpr (kWithA) {
+        src.a_src(ta, &ra, &sa);
+        sa = __builtin_amdgcn_readfirstlane(sa);
+      }
+      if constexpr (kWithB) {
+        src.b_src(tb, &rb, &sb);
+        sb = __builtin_amdgcn_readfirstlane(sb);
+      }
     }
     __device__ __forceinline__ void operator()(int q) const {
       if (q < kA) {
@@ -301,28 +298,29 @@ struct DmaMainloop {
     }
   };
 
-  // The loads step t issues for step u = t + STAGES - 1 (or, in the
-  // prologue, for step u itself).
+  // Unpaired: the loads of K step u, A and B.
   template <class Src>
   __device__ __forceinline__ static StepDma<Src, true> step_dma(uint8_t* __restrict__ lds, int u, const Src& src) {
-    return StepDma<Src, true>(a_slot(lds, u), Cfg::APAIR ? u - 1 : u, b_slot(lds, u), u, src);
+    return StepDma<Src, true>(a_slot(lds, u), u, b_slot(lds, u), u, src);
+  }
+  // Paired: A pair m's loads (from K step 2m) with step u's B, or u's B only.
+  template <class Src>
+  __device__ __forceinline__ static StepDma<Src, true> pair_dma(uint8_t* __restrict__ lds, int m, int u,
+                                                               const Src& src) {
+    return StepDma<Src, true>(a_slot(lds, 2 * m), 2 * m, b_slot(lds, u), u, src);
   }
   template <class Src>
-  __device__ __forceinline__ static StepDma<Src, false> step_dma_b(uint8_t* __restrict__ lds, int u, const Src& src) {
+  __device__ __forceinline__ static StepDma<Src, false> b_dma(uint8_t* __restrict__ lds, int u, const Src& src) {
     return StepDma<Src, false>(nullptr, 0, b_slot(lds, u), u, src);
   }
-
   template <class Src>
-  __device__ __forceinline__ static void issue(uint8_t* __restrict__ lds, int u, const Src& src) {
-    if (!Cfg::APAIR || (u & 1) != 0) {
-      const auto dma = step_dma(lds, u, src);
+  __device__ __forceinline__ static StepDma<Src, true, false> a_dma(uint8_t* __restrict__ lds, int m, const Src& src) {
+    return StepDma<Src, true, false>(a_slot(lds, 2 * m), 2 * m, nullptr, 0, src);
+  }
+  template <class Dma>
+  __device__ __forceinline__ static void issue_all(const Dma& dma) {
 #pragma unroll
-      for (int q = 0; q < dma.kCount; ++q) dma(q);
-    } else {
-      const auto dma = step_dma_b(lds, u, src);
-#pragma unroll
-      for (int q = 0; q < dma.kCount; ++q) dma(q);
-    }
+    for (int q = 0; q < Dma::kCount; ++q) dma(q);
   }
 
   struct NoDma {
@@ -480,22 +478,47 @@ struct DmaMainloop {
     }
   }
 
-  // With APAIR, the wait at step t of the last STAGES-1 steps, when the
-  // `later` steps after t (all issued) are the last ones of the tile and
-  // the step count is even: odd t, those steps' B and the A pairs of the
-  // odd ones among them; even t (later is odd), its pair's A came with
-  // step t+1's B, so that B and the later-1 steps after it.
-  template <int L>
-  __device__ __forceinline__ static void wait_pair_tail(int later, bool t_odd) {
-    if constexpr (L > Cfg::STAGES - 2) {
-      wait_vmcnt<0>();
-    } else {
-      if (later == L) {
-        if (t_odd) wait_vmcnt<L * Cfg::kBInstr + (L / 2) * Cfg::kAInstr>();
-        else wait_vmcnt<L * Cfg::kBInstr + ((L > 0 ? L - 1 : 0) / 2) * Cfg::kAInstr>();
-      } else {
-        wait_pair_tail<L + 1>(later, t_odd);
-      }
+  // Paired schedule (APAIR), for an even step count n: the prologue loads
+  // A pair 0, then B of steps 0 .. STAGES-2. Step t then loads B of step
+  // t+STAGES-1 and, if t is even, A pair t/2+1 (A first), each while it
+  // exists: an A slot is refilled once the pair before it has been read to
+  // its end, so A runs two steps ahead and B STAGES-1. The wait at the top
+  // of step t counts the loads issued after step t's last one: B of the
+  // STAGES-2 steps after it (the last of them issued with A pair t/2 when t
+  // is even and STAGES is 4), plus, for odd t, the A pair its successor
+  // step issued. In the last steps fewer loads follow: with STAGES 4 the
+  // last four steps wait for 2B (and load A pair n/2-1 and the last B), A+2B,
+  // B and nothing; with STAGES 3 the last two wait for B and nothing (and so
+  // do the only two steps of n = 2 with STAGES 4).
+  template <class Src>
+  __device__ __forceinline__ static void run_paired(uint8_t* lds, const Src& src, int n, Acc& acc) {
+    constexpr int S = Cfg::STAGES;
+    issue_all(a_dma(lds, 0, src));
+#pragma unroll
+    for (int u = 0; u < S - 1; ++u)
+      if (u < n) issue_all(b_dma(lds, u, src));
+    int t = 0;
+    for (; t + S < n; t += 2) {
+      wait_vmcnt<Cfg::kLaterLoadsEven>();
+      __builtin_amdgcn_s_barrier();
+      compute(a_slot(lds, t), b_slot(lds, t), 0, acc, pair_dma(lds, t / 2 + 1, t + S - 1, src));
+      wait_vmcnt<Cfg::kLaterLoadsOdd>();
+      __builtin_amdgcn_s_barrier();
+      compute(a_slot(lds, t + 1), b_slot(lds, t + 1), 1, acc, b_dma(lds, t + S, src));
+    }
+    if (S == 4 && t + 2 < n) {  // t = n - 4, the last step that loads (n = 2 has none)
+      wait_vmcnt<2 * Cfg::kBInstr>();
+      __builtin_amdgcn_s_barrier();
+      compute(a_slot(lds, t), b_slot(lds, t), 0, acc, pair_dma(lds, t / 2 + 1, t + 3, src));
+      ++t;
+    }
+    for (; t < n; ++t) {  // nothing left to load; `later` steps follow
+      const int later = n - 1 - t;
+      if (later >= 2) wait_vmcnt<Cfg::kAInstr + 2 * Cfg::kBInstr>();
+      else if (later == 1) wait_vmcnt<Cfg::kBInstr>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      compute(a_slot(lds, t), b_slot(lds, t), t & 1, acc);
     }
   }
 
@@ -508,44 +531,27 @@ struct DmaMainloop {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[jn][i][v] = 0.0f;
     if (num_steps <= 0) return;
+    if constexpr (Cfg::APAIR) {
+      run_paired(lds, src, num_steps, acc);
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < Cfg::STAGES - 1; ++s)
-      if (s < num_steps) issue(lds, s, src);
+      if (s < num_steps) issue_all(step_dma(lds, s, src));
     if constexpr (Cfg::PIPE == 3 || Cfg::PIPE == 4) {
       // Steps that issue a later step's loads, among their MFMAs; at the top
       // of each, the loads of steps t .. t+STAGES-2 have been issued.
       int t = 0;
-      if constexpr (Cfg::APAIR) {
-        // Steps in pairs, even then odd: STAGES is even, so the even step
-        // issues an odd step's loads (B and its pair's A) and the odd step
-        // an even one's (B only).
-        for (; t + Cfg::STAGES < num_steps; t += 2) {
-          wait_vmcnt<Cfg::kLaterLoadsEven>();
-          __builtin_amdgcn_s_barrier();
-          compute(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + Cfg::STAGES - 1, src));
-          wait_vmcnt<Cfg::kLaterLoadsOdd>();
-          __builtin_amdgcn_s_barrier();
-          compute(a_slot(lds, t + 1), b_slot(lds, t + 1), 1, acc, step_dma_b(lds, t + Cfg::STAGES, src));
-        }
-        if (t + Cfg::STAGES - 1 < num_steps) {  // the last step that issues (even)
-          wait_vmcnt<Cfg::kLaterLoadsEven>();
-          __builtin_amdgcn_s_barrier();
-          compute(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + Cfg::STAGES - 1, src));
-          ++t;
-        }
-      } else {
-        for (; t + Cfg::STAGES - 1 < num_steps; ++t) {
-          wait_vmcnt<Cfg::kLaterLoads>();
-          __builtin_amdgcn_s_barrier();
-          compute(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + Cfg::STAGES - 1, src));
-        }
+      for (; t + Cfg::STAGES - 1 < num_steps; ++t) {
+        wait_vmcnt<Cfg::kLaterLoads>();
+        __builtin_amdgcn_s_barrier();
+        compute(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + Cfg::STAGES - 1, src));
       }
       // The last STAGES-1 steps issue nothing.
       for (; t < num_steps; ++t) {
-        if constexpr (Cfg::APAIR) wait_pair_tail<0>(num_steps - 1 - t, (t & 1) != 0);
-        else wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(num_steps - 1 - t);
+        wait_steps<Cfg::kLoadsPerStep, Cfg::STAGES - 2>(num_steps - 1 - t);
         __builtin_amdgcn_s_barrier();
-        compute(a_slot(lds, t), b_slot(lds, t), Cfg::APAIR ? (t & 1) : 0, acc);
+        compute(a_slot(lds, t), b_slot(lds, t), 0, acc);
       }
       return;
     }
@@ -556,7 +562,7 @@ struct DmaMainloop {
       // Every wave's step-t data is in LDS, and every wave is done with
       // step t-1's stage, which the next issue overwrites.
       __builtin_amdgcn_s_barrier();
-      if (t + Cfg::STAGES - 1 < num_steps) issue(lds, t + Cfg::STAGES - 1, src);
+      if (t + Cfg::STAGES - 1 < num_steps) issue_all(step_dma(lds, t + Cfg::STAGES - 1, src));
       compute(a_slot(lds, t), b_slot(lds, t), 0, acc);
     }
   }

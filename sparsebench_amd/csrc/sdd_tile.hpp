@@ -128,12 +128,12 @@ __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, in
 // the benchmark configurations (MI355X, samples interleaved across shapes):
 // 128 x 512 tiles of 8 waves (64 x 128 each: 8 MFMAs per 16-deep sub-step,
 // enough to cover the LDS fragment reads), BK 32 through a 3-stage ring, or
-// a 4-stage one for a deep reduction (D >= 4096), which loads the x rows two
-// K steps at a time as whole 128-byte rows (APAIR); 128 x 256 tiles (BK 64 x 3
+// a 4-stage one for a deep reduction (D >= 4096), the x rows loaded two K
+// steps at a time as whole 128-byte rows (APAIR); 128 x 256 tiles (BK 64 x 3
 // stages) when F is not a multiple of 512. All: non-temporal W1 loads, the
 // DMA of the step two ahead and the next sub-step's fragment reads issued
 // among the MFMAs (PIPE 3).
-using SddWideTile = DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3>;
+using SddWideTile = DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3, 1, 1>;
 using SddDeepTile = DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 3, 1, 1>;
 using SddNarrowTile = DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 3>;
 

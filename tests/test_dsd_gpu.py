@@ -56,8 +56,8 @@ def test_oracle_matches_dense_reference() -> None:
 @pytest.mark.parametrize("version", [1, 4, 5])
 @pytest.mark.parametrize("case", CASE_NAMES)
 @pytest.mark.parametrize("bs", [64, 128])
-@pytest.mark.parametrize(("num_experts", "f_blocks"), [(8, 1), (8, 4), (64, 1), (64, 2)],
-                         ids=["E8F1", "E8F4", "E64F1", "E64F2"])
+@pytest.mark.parametrize(("num_experts", "f_blocks"), [(8, 1), (8, 4), (64, 1), (64, 2), (8, 3)],
+                         ids=["E8F1", "E8F4", "E64F1", "E64F2", "E8F3"])
 @pytest.mark.parametrize("d_model", [128, 256, 512], ids=["D128", "D256", "D512"])
 def test_matches_oracle(version, case, bs, num_experts, f_blocks, d_model) -> None:
     if not supports(version, bs, d_model):

@@ -58,6 +58,14 @@ CASES = {
     "few_experts": (lambda s: routing_case("random", 2048, 4, seed=s), 4, 256, 512),
 }
 
+# SDD-only cases (D % 256 != 0 leaves the DSD's layer tiles out): short
+# reductions for the paired-A main loop, D = 64 and 192 being 2 and 6 K steps
+# of 32 (the shortest, and one pair past a multiple of 4).
+SDD_CASES = {
+    "short_d64": (lambda s: routing_case("random", 1000, 16, seed=s), 16, 64, 512),
+    "short_d192": (lambda s: routing_case("zipf", 1000, 16, seed=s), 16, 192, 512),
+}
+
 
 def real_rows(topo) -> np.ndarray:
     """Padded row indices that hold a copy, from the device layout."""
@@ -90,7 +98,7 @@ def dense_rows(blocks: torch.Tensor, ffn_blocks: int) -> torch.Tensor:
 
 
 def inputs(case: str, seed: int):
-    build, e, d, f = CASES[case]
+    build, e, d, f = CASES[case] if case in CASES else SDD_CASES[case]
     g = torch.Generator().manual_seed(100 + seed)
     idx = build(seed)
     t = idx.shape[0]
@@ -101,7 +109,7 @@ def inputs(case: str, seed: int):
 
 
 @pytest.mark.parametrize("gate", GATES)
-@pytest.mark.parametrize("case", list(CASES))
+@pytest.mark.parametrize("case", list(CASES) + list(SDD_CASES))
 def test_sdd_experts_rows_equal_row_block_kernel(monkeypatch, gate: str, case: str) -> None:
     from sparsebench_amd import _C
     from sparsebench_amd.routing import route_device
@@ -119,7 +127,7 @@ def test_sdd_experts_rows_equal_row_block_kernel(monkeypatch, gate: str, case: s
     pad = torch.as_tensor(chunk_pad_rows(topo, SDD_RMAX), device="cuda")
     if pad.numel():
         assert torch.all(h_ex[pad] == 0)
-    if case == "edges":  # and against the oracle directly
+    if case == "edges" or case in SDD_CASES:  # and against the oracle directly
         lay = build_layout(idx.numpy(), e, f, 128)
         ref = dense_rows(sdd_blocks(x.float(), w1.float(), lay), f // 128)
         live = rows[rows < ref.shape[0]].cpu()

@@ -40,8 +40,8 @@ def run_sdd(idx, x, w1, gelu: bool = True):
 
 @pytest.mark.parametrize("case", CASE_NAMES)
 @pytest.mark.parametrize(("num_experts", "d_model", "ffn_dim"),
-                         [(8, 128, 256), (8, 320, 512), (64, 64, 256), (4, 1024, 4096)],
-                         ids=["E8D128F256", "E8D320F512", "E64D64F256", "E4D1024F4096"])
+                         [(8, 128, 256), (8, 320, 512), (64, 64, 256), (4, 1024, 4096), (8, 64, 512), (8, 192, 512)],
+                         ids=["E8D128F256", "E8D320F512", "E64D64F256", "E4D1024F4096", "E8D64F512", "E8D192F512"])
 def test_sdd_matches_oracle(case: str, num_experts: int, d_model: int, ffn_dim: int) -> None:
     idx, x, w1 = make_inputs(case, 300, num_experts, d_model, ffn_dim)
     torch.testing.assert_close(run_sdd(idx, x, w1).float().cpu(), expected(idx, x, w1), **TOL)

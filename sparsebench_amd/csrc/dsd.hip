@@ -49,14 +49,16 @@ int launch_dsd(const void* blocks, const void* w, const int32_t* row_offsets, co
 //   D % 256 == 0   128 x 256 tiles, BK 64 x 3 stages, 8 waves
 //   otherwise      128 x 128 tiles, BK 64 x 3 stages, 4 waves
 // All with non-temporal W loads; the 256- and 512-wide ones issue the DMA of
-// the step ahead and the next sub-step's fragment reads among the MFMAs, and
+// a later step and the next sub-step's fragment reads among the MFMAs, and
 // the 512-wide ones load H two K steps at a time, as whole 128-byte rows
-// (APAIR; a row's K is a multiple of 64, since bs is 64 or 128).
+// (APAIR; a row's K is a multiple of 64, since bs is 64 or 128), and read
+// the next step's first fragments among the current step's last MFMAs
+// (PIPE 5).
 template <int BM, class... Args>
 int dispatch_dsd(int64_t d_model, int64_t row_k, Args... args) {
   if (d_model % 512 == 0) {
-    if (row_k >= 8192) return launch_dsd<DmaCfg<BM, 512, 32, 4, 2, 4, 0, 2, 3, 1, 1>>(args...);
-    return launch_dsd<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 3, 1, 1>>(args...);
+    if (row_k >= 8192) return launch_dsd<DmaCfg<BM, 512, 32, 4, 2, 4, 0, 2, 5, 1, 1>>(args...);
+    return launch_dsd<DmaCfg<BM, 512, 32, 4, 1, 4, 0, 2, 5, 1, 1>>(args...);
   }
   if (d_model % 256 == 0) return launch_dsd<DmaCfg<BM, 256, 64, 3, 2, 4, 0, 2, 3>>(args...);
   return launch_dsd<DmaCfg<BM, 128, 64, 3, 2, 2, 0, 2, 0>>(args...);

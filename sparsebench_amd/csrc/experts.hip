@@ -49,14 +49,15 @@ namespace {
 
 // Main-loop configuration of an R-group tile: M = 32 R, K steps of 32, one
 // row of WAVES waves, non-temporal weight loads, DMA issue spread over the
-// MFMAs (PIPE 3). With 8 waves (two per SIMD, at most 256 registers each)
-// and six row groups, the 192 accumulators leave room for one set of A
-// fragments only (PIPE 4); a bf16 tile over 160 KB is staged in two parts.
+// MFMAs and the next step's first fragments read among the current step's
+// last MFMAs (PIPE 5). With 8 waves (two per SIMD, at most 256 registers
+// each) and six row groups, the 192 accumulators leave room for one set of
+// A fragments only (PIPE 4); a bf16 tile over 160 KB is staged in two parts.
 // 4-stage rings load A two K steps at a time, as whole 128-byte rows
 // (APAIR); in the 3-stage rings of the taller SDD tiles the extra address
 // registers would spill inside the main loop.
 template <int R, int BN, int WAVES, int STAGES>
-using ChunkCfg = DmaCfg<32 * R, BN, 32, STAGES, 1, WAVES, 0, 2, (WAVES == 8 && R >= 6) ? 4 : 3,
+using ChunkCfg = DmaCfg<32 * R, BN, 32, STAGES, 1, WAVES, 0, 2, (WAVES == 8 && R >= 6) ? 4 : 5,
                         (32 * R * BN * 2 > 160 * 1024) ? 2 : 1, STAGES == 4 ? 1 : 0>;
 
 // LDS of the expert tiles of a kernel: the largest over its tile heights.

@@ -53,6 +53,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            kBufferFlags);
 }
 
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  // gfx9 encoding of s_waitcnt lgkmcnt(0), vmcnt and expcnt left at their maximum.
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
@@ -73,7 +78,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // address unit takes them, which delays its MFMAs). 4: as 3 with the A
 // fragments single-buffered: each is read again for the next sub-step
 // right after its last MFMA of this one (TM x 4 fewer registers, for tall
-// tiles whose accumulators leave no room for a second set).
+// tiles whose accumulators leave no room for a second set). 5: as 3, with
+// the wait and barrier of step t+1 moved into step t's last sub-step, ahead
+// of its MFMAs, and step t+1's first fragments read among them: otherwise
+// every step starts with a barrier and LDS reads and no MFMA to cover them.
 // EPI_PARTS: the epilogue stages the bf16 tile through LDS in this many
 // parts of BM / EPI_PARTS rows (a 192 x 512 tile does not fit at once).
 // APAIR: A is loaded two K steps at a time, as whole 128-byte rows (BK 32):
@@ -131,7 +139,7 @@ struct DmaCfg {
   static_assert(STAGES >= 2 && STAGES <= 8, "STAGES");
   static_assert(kLdsAlloc <= 160 * 1024, "LDS");
   static_assert((APAIR ? kLaterLoadsOdd : kLaterLoads) <= 63, "vmcnt");
-  static_assert(!APAIR || (BK == 32 && (STAGES == 3 || STAGES == 4) && (PIPE == 3 || PIPE == 4)),
+  static_assert(!APAIR || (BK == 32 && (STAGES == 3 || STAGES == 4) && (PIPE == 3 || PIPE == 4 || PIPE == 5)),
                 "paired A: BK 32, a 3- or 4-stage B ring, DMA among the MFMAs");
   static_assert(EPI_PARTS == 1 || (WM == 1 && TM % EPI_PARTS == 0), "epilogue parts of whole row groups");
 };
@@ -333,44 +341,45 @@ struct DmaMainloop {
     compute(as, bs, khalf, acc, NoDma{});
   }
 
-  // One K step's fragments and MFMAs, from A slot `as` (K half `khalf` of
-  // it with APAIR, else 0) and B slot `bs`. With PIPE 3 and 4, dma(q) for
-  // q < Dma::kCount is called among the MFMAs (a later step's loads, into
-  // other slots), spread evenly by the scheduling groups.
-  template <class Dma>
-  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ as, const uint8_t* __restrict__ bs,
-                                                 int khalf, Acc& acc, const Dma& dma) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-    const int h = lane >> 5;
-    const int kc = 4 * khalf + h;  // this lane's first 8-wide K chunk of the step in the A row
-    // A side: row m = wm*WTM + 32 i + lane % 32.
-    int a_row_off[Cfg::TM], a_swz[Cfg::TM];
+  // The lane's LDS offsets for its MMA fragments, fixed for the tile.
+  //   A side (MFMA src B): row m = wm*WTM + 32 i + lane % 32, 8 k values
+  //   of chunk 2s + kc, kc = 4 khalf + lane / 32.
+  //   W side (MFMA src A): lane j of its 16-group reads row (k0 + j/4),
+  //   columns n0 + 16 (group % 2) + 4 (j % 4); chunk block (4 chunks =
+  //   64 B) of n block jn is XORed with (k & 3) = j / 4.
+  struct Frags {
+    int a_row_off[Cfg::TM], a_swz[Cfg::TM], b_off[Cfg::TN];
+    int h;
+    __device__ __forceinline__ Frags() {
+      const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+      const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+      h = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < Cfg::TM; ++i) {
-      const int r = wm * Cfg::WTM + 32 * i + (lane & 31);
-      a_row_off[i] = r * Cfg::kARowBytes;
-      a_swz[i] = swz_a<Cfg::kABK>(r);
+      for (int i = 0; i < Cfg::TM; ++i) {
+        const int r = wm * Cfg::WTM + 32 * i + (lane & 31);
+        a_row_off[i] = r * Cfg::kARowBytes;
+        a_swz[i] = swz_a<Cfg::kABK>(r);
+      }
+      const int g = lane >> 4, jj = lane & 15;
+      const int krow = 8 * (g >> 1) + (jj >> 2);
+#pragma unroll
+      for (int jn = 0; jn < Cfg::TN; ++jn) {
+        const int blk = (wn * Cfg::WTN) / 32 + jn;  // 32-column block index
+        const int chunk = 4 * (blk ^ (jj >> 2)) + 2 * (g & 1) + ((jj & 3) >> 1);
+        b_off[jn] = krow * Cfg::kBRowBytes + chunk * 16 + (jj & 1) * 8;
+      }
     }
-    // W side: lane j of its 16-group reads row (k0 + j/4), columns
-    // n0 + 16 (group % 2) + 4 (j % 4); chunk block (4 chunks = 64 B) of
-    // n block jn is XORed with (k & 3) = j / 4.
-    const int g = lane >> 4, jj = lane & 15;
-    const int krow = 8 * (g >> 1) + (jj >> 2);
-    int b_off[Cfg::TN];
-#pragma unroll
-    for (int jn = 0; jn < Cfg::TN; ++jn) {
-      const int blk = (wn * Cfg::WTN) / 32 + jn;                // 32-column block index
-      const int chunk = 4 * (blk ^ (jj >> 2)) + 2 * (g & 1) + ((jj & 3) >> 1);
-      b_off[jn] = krow * Cfg::kBRowBytes + chunk * 16 + (jj & 1) * 8;
+    // Sub-step s's A fragment of row group i (K half `khalf` of a paired slot).
+    __device__ __forceinline__ bf16x8_t read_a1(const uint8_t* __restrict__ as, int khalf, int s, int i) const {
+      const int kc = 4 * khalf + h;
+      return *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * s + kc) ^ a_swz[i]) << 4));
     }
-    constexpr int kSub = Cfg::BK / 16;
-    auto read_a = [&](int s, bf16x8_t (&a)[Cfg::TM]) {
+    __device__ __forceinline__ void read_a(const uint8_t* __restrict__ as, int khalf, int s,
+                                           bf16x8_t (&a)[Cfg::TM]) const {
 #pragma unroll
-      for (int i = 0; i < Cfg::TM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * s + kc) ^ a_swz[i]) << 4));
-    };
-    auto read_b = [&](int s, bf16x8_t (&b)[Cfg::TN]) {
+      for (int i = 0; i < Cfg::TM; ++i) a[i] = read_a1(as, khalf, s, i);
+    }
+    __device__ __forceinline__ void read_b(const uint8_t* __restrict__ bs, int s, bf16x8_t (&b)[Cfg::TN]) const {
 #pragma unroll
       for (int jn = 0; jn < Cfg::TN; ++jn) {
         const uint8_t* p = bs + b_off[jn] + 16 * s * Cfg::kBRowBytes;
@@ -378,19 +387,31 @@ struct DmaMainloop {
         const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * Cfg::kBRowBytes));
         b[jn] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
-    };
-    auto mfmas = [&](const bf16x8_t (&a)[Cfg::TM], const bf16x8_t (&b)[Cfg::TN]) {
+    }
+  };
+  __device__ __forceinline__ static void mfmas(Acc& acc, const bf16x8_t (&a)[Cfg::TM], const bf16x8_t (&b)[Cfg::TN]) {
 #pragma unroll
-      for (int jn = 0; jn < Cfg::TN; ++jn)
+    for (int jn = 0; jn < Cfg::TN; ++jn)
 #pragma unroll
-        for (int i = 0; i < Cfg::TM; ++i)
-          acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[jn], a[i], acc[jn][i], 0, 0, 0);
-    };
+      for (int i = 0; i < Cfg::TM; ++i)
+        acc[jn][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[jn], a[i], acc[jn][i], 0, 0, 0);
+  }
+
+  // One K step's fragments and MFMAs, from A slot `as` (K half `khalf` of
+  // it with APAIR, else 0) and B slot `bs`. With PIPE 3 and 4, dma(q) for
+  // q < Dma::kCount is called among the MFMAs (a later step's loads, into
+  // other slots), spread evenly by the scheduling groups.
+  template <class Dma>
+  __device__ __forceinline__ static void compute(const uint8_t* __restrict__ as, const uint8_t* __restrict__ bs,
+                                                 int khalf, Acc& acc, const Dma& dma) {
+    const Frags fr;
+    constexpr int kSub = Cfg::BK / 16;
+    auto read_a = [&](int s, bf16x8_t (&a)[Cfg::TM]) { fr.read_a(as, khalf, s, a); };
+    auto read_b = [&](int s, bf16x8_t (&b)[Cfg::TN]) { fr.read_b(bs, s, b); };
+    auto mfmas = [&](const bf16x8_t (&a)[Cfg::TM], const bf16x8_t (&b)[Cfg::TN]) { DmaMainloop::mfmas(acc, a, b); };
     if constexpr (Cfg::PIPE == 4) {
       constexpr int kDma = Dma::kCount;
-      auto read_a1 = [&](int sub, int i) {
-        return *reinterpret_cast<const bf16x8_t*>(as + a_row_off[i] + (((2 * sub + kc) ^ a_swz[i]) << 4));
-      };
+      auto read_a1 = [&](int sub, int i) { return fr.read_a1(as, khalf, sub, i); };
       bf16x8_t a[Cfg::TM], b[2][Cfg::TN];
       read_a(0, a);
       read_b(0, b[0]);
@@ -478,6 +499,132 @@ struct DmaMainloop {
     }
   }
 
+  using FragA = bf16x8_t[2][Cfg::TM];
+  using FragB = bf16x8_t[2][Cfg::TN];
+
+  // PIPE 5: one K step whose first sub-step's fragments are already in
+  // a[0] / b[0]. The sub-steps before the last read the next sub-step's
+  // fragments and issue this step's DMA among their MFMAs. The last one
+  // first completes this step's LDS reads, waits for the next step's loads
+  // (wait()), passes the barrier and reads the next step's first fragments
+  // (slots nas / nbs) into a[0] / b[0], and then runs its MFMAs over those
+  // reads' latency. All of this step's loads are issued before the wait, so
+  // its counts are the ones a wait at the top of the next step would use.
+  template <bool kNext, class Dma, class Wait>
+  __device__ __forceinline__ static void compute_xs(const uint8_t* __restrict__ as, const uint8_t* __restrict__ bs,
+                                                    int khalf, Acc& acc, const Dma& dma, const Frags& fr, FragA& a,
+                                                    FragB& b, const uint8_t* __restrict__ nas,
+                                                    const uint8_t* __restrict__ nbs, int nkhalf, const Wait& wait) {
+    constexpr int kSub = Cfg::BK / 16;
+    static_assert(kSub % 2 == 0, "the last sub-step uses the second register set");
+    constexpr int kMfma = Cfg::TM * Cfg::TN;
+    constexpr int kReads = Cfg::TM + 2 * Cfg::TN;
+    constexpr int kPer = (kReads + kMfma - 1) / kMfma;
+    constexpr int kDma = Dma::kCount;
+    auto mfmas = [&](const bf16x8_t (&fa)[Cfg::TM], const bf16x8_t (&fb)[Cfg::TN]) { DmaMainloop::mfmas(acc, fa, fb); };
+    static_for<0, kSub>([&](auto sc) {
+      constexpr int s = decltype(sc)::value;
+      if constexpr (s + 1 < kSub) {
+        fr.read_a(as, khalf, s + 1, a[(s + 1) & 1]);
+        fr.read_b(bs, s + 1, b[(s + 1) & 1]);
+        mfmas(a[s & 1], b[s & 1]);
+        constexpr int q0 = s * kDma / (kSub - 1), q1 = (s + 1) * kDma / (kSub - 1);
+#pragma unroll
+        for (int q = q0; q < q1; ++q) dma(q);
+        sched_substep_with_dma<0, kMfma, kReads, kPer, q1 - q0>();
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        if constexpr (kNext) {
+          wait_lgkmcnt0();  // this step's slots are read to their end before the barrier
+          wait();
+          __builtin_amdgcn_s_barrier();
+          fr.read_a(nas, nkhalf, 0, a[0]);
+          fr.read_b(nbs, 0, b[0]);
+        }
+        mfmas(a[s & 1], b[s & 1]);
+        if constexpr (kNext) sched_interleave<0, kMfma, kReads, kPer>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
+  }
+
+  struct NoWait {
+    __device__ __forceinline__ void operator()() const {}
+  };
+  template <int N>
+  struct WaitVm {
+    __device__ __forceinline__ void operator()() const { wait_vmcnt<N>(); }
+  };
+
+  // PIPE 5, paired A: the schedule of run_paired, each step's wait and
+  // barrier moved into the step before it.
+  template <class Src>
+  __device__ __forceinline__ static void run_paired_xs(uint8_t* lds, const Src& src, int n, Acc& acc) {
+    constexpr int S = Cfg::STAGES;
+    constexpr int kA = Cfg::kAInstr, kB = Cfg::kBInstr;
+    const Frags fr;
+    FragA a;
+    FragB b;
+    issue_all(a_dma(lds, 0, src));
+#pragma unroll
+    for (int u = 0; u < S - 1; ++u)
+      if (u < n) issue_all(b_dma(lds, u, src));
+    if (S == 4 && n == 2) wait_vmcnt<kB>();
+    else wait_vmcnt<Cfg::kLaterLoadsEven>();
+    __builtin_amdgcn_s_barrier();
+    fr.read_a(a_slot(lds, 0), 0, 0, a[0]);
+    fr.read_b(b_slot(lds, 0), 0, b[0]);
+    int t = 0;
+    for (; t + S < n; t += 2) {
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), 0, acc, pair_dma(lds, t / 2 + 1, t + S - 1, src), fr, a, b,
+                       a_slot(lds, t + 1), b_slot(lds, t + 1), 1, WaitVm<Cfg::kLaterLoadsOdd>{});
+      compute_xs<true>(a_slot(lds, t + 1), b_slot(lds, t + 1), 1, acc, b_dma(lds, t + S, src), fr, a, b,
+                       a_slot(lds, t + 2), b_slot(lds, t + 2), 0, WaitVm<Cfg::kLaterLoadsEven>{});
+    }
+    if (S == 4 && t + 2 < n) {  // t = n - 4, the last step that loads
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), 0, acc, pair_dma(lds, t / 2 + 1, t + 3, src), fr, a, b,
+                       a_slot(lds, t + 1), b_slot(lds, t + 1), 1, WaitVm<kA + 2 * kB>{});
+      ++t;
+    }
+    for (; t + 1 < n; ++t) {  // nothing left to load; the step after t has n - 2 - t after it
+      const int later = n - 2 - t;
+      auto w = [later] {
+        if (later >= 2) wait_vmcnt<kA + 2 * kB>();
+        else if (later == 1) wait_vmcnt<kB>();
+        else wait_vmcnt<0>();
+      };
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), t & 1, acc, NoDma{}, fr, a, b, a_slot(lds, t + 1),
+                       b_slot(lds, t + 1), (t + 1) & 1, w);
+    }
+    compute_xs<false>(a_slot(lds, t), b_slot(lds, t), t & 1, acc, NoDma{}, fr, a, b, nullptr, nullptr, 0, NoWait{});
+  }
+
+  // PIPE 5, unpaired.
+  template <class Src>
+  __device__ __forceinline__ static void run_xs(uint8_t* lds, const Src& src, int n, Acc& acc) {
+    constexpr int S = Cfg::STAGES;
+    const Frags fr;
+    FragA a;
+    FragB b;
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+      if (s < n) issue_all(step_dma(lds, s, src));
+    wait_steps<Cfg::kLoadsPerStep, S - 2>(n - 1);
+    __builtin_amdgcn_s_barrier();
+    fr.read_a(a_slot(lds, 0), 0, 0, a[0]);
+    fr.read_b(b_slot(lds, 0), 0, b[0]);
+    int t = 0;
+    for (; t + S - 1 < n; ++t)
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), 0, acc, step_dma(lds, t + S - 1, src), fr, a, b,
+                       a_slot(lds, t + 1), b_slot(lds, t + 1), 0, WaitVm<Cfg::kLaterLoads>{});
+    for (; t + 1 < n; ++t) {
+      const int later = n - 2 - t;
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), 0, acc, NoDma{}, fr, a, b, a_slot(lds, t + 1),
+                       b_slot(lds, t + 1), 0, [later] { wait_steps<Cfg::kLoadsPerStep, S - 2>(later); });
+    }
+    compute_xs<false>(a_slot(lds, t), b_slot(lds, t), 0, acc, NoDma{}, fr, a, b, nullptr, nullptr, 0, NoWait{});
+  }
+
   // Paired schedule (APAIR), for an even step count n: the prologue loads
   // A pair 0, then B of steps 0 .. STAGES-2. Step t then loads B of step
   // t+STAGES-1 and, if t is even, A pair t/2+1 (A first), each while it
@@ -531,6 +678,11 @@ struct DmaMainloop {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[jn][i][v] = 0.0f;
     if (num_steps <= 0) return;
+    if constexpr (Cfg::PIPE == 5) {
+      if constexpr (Cfg::APAIR) run_paired_xs(lds, src, num_steps, acc);
+      else run_xs(lds, src, num_steps, acc);
+      return;
+    }
     if constexpr (Cfg::APAIR) {
       run_paired(lds, src, num_steps, acc);
       return;

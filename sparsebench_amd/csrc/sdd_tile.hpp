@@ -131,10 +131,12 @@ __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, in
 // a 4-stage one for a deep reduction (D >= 4096), the x rows loaded two K
 // steps at a time as whole 128-byte rows (APAIR); 128 x 256 tiles (BK 64 x 3
 // stages) when F is not a multiple of 512. All: non-temporal W1 loads, the
-// DMA of the step two ahead and the next sub-step's fragment reads issued
-// among the MFMAs (PIPE 3).
+// DMA of a later step and the next sub-step's fragment reads issued among
+// the MFMAs (PIPE 3); the 4-stage tile also reads the next step's first
+// fragments among the current step's last MFMAs (PIPE 5; in the 3-stage
+// one that schedule spills inside the main loop).
 using SddWideTile = DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3, 1, 1>;
-using SddDeepTile = DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 3, 1, 1>;
+using SddDeepTile = DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 5, 1, 1>;
 using SddNarrowTile = DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 3>;
 
 enum class SddTile { kWide, kDeep, kNarrow };

@@ -3,7 +3,7 @@ computing it on the same MI355X (the measurements of the reference's
 bench/bench_moe.py and bench/bench_token_rounding.py, made here).
 
     python bench_baselines.py                 # both tables, markdown on stdout
-    python bench_baselines.py --only layer    # or: --only rounding, --only replay, --only ceilings
+    python bench_baselines.py --only layer    # or: --only rounding, --only replay, --only ceilings, --only gemm
 
 Layer pipelines (everything from the routing to the [T, D] output is timed,
 host syncs included):
@@ -30,7 +30,8 @@ moe_forward at T'.
 Ceilings (the box's practical roofs, next to the published 8 TB/s and
 2.5 PFLOP/s): streaming reads of 2 GiB with 16-byte vector loads and through
 LDS DMA (sbp_read of libsparsebench_probe.so, the load path of SDD / DSD), a 1 GiB device copy, and
-dense bf16 GEMMs through torch.matmul (hipBLASLt).
+dense bf16 GEMMs through torch.matmul (hipBLASLt), with the weight as the
+layer stores it ([K, N]) and transposed ([N, K]); --only gemm runs just these.
 
 Every pipeline is checked against the fp32 loop reference before it is
 timed (max error <= 3e-2 (1 + max |ref|), the reference's check). Timing: a
@@ -277,20 +278,31 @@ def ceilings_table(flush: torch.Tensor) -> list[str]:
     print(lines[-1], flush=True)
     del data, src, dst
     torch.cuda.empty_cache()
+    return lines + gemm_table(flush, header=False)
+
+
+def gemm_table(flush: torch.Tensor, header: bool = True) -> list[str]:
+    """Dense bf16 GEMMs of the Mixtral-like stages' total shapes through torch.matmul (hipBLASLt), with the
+    weight stored as the layer stores it (N-contiguous, [K, N]) and transposed (K-contiguous, [N, K])."""
+    lines = ["| measurement | ms | rate | of published peak |", "|---|---:|---:|---:|"] if header else []
+    if header:
+        print("\n".join(lines), flush=True)
     for m, n, k in ((8192, 8192, 8192), (8192, 14336, 4096), (8192, 4096, 14336)):
         a = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
         b = torch.randn(k, n, device="cuda", dtype=torch.bfloat16)
-        ms = time_ms(lambda: a @ b, flush)
-        tf = 2 * m * n * k / ms / 1e9
-        lines.append(f"| bf16 GEMM {m}x{n}x{k} (torch.matmul) | {ms:.3f} | {tf:.0f} TFLOP/s | {tf / 2500:.0%} |")
-        print(lines[-1], flush=True)
-        del a, b
+        bt = b.t().contiguous()
+        for label, fn in (("weight [K, N]", lambda: a @ b), ("weight [N, K]", lambda: a @ bt.t())):
+            ms = time_ms(fn, flush)
+            tf = 2 * m * n * k / ms / 1e9
+            lines.append(f"| bf16 GEMM {m}x{n}x{k}, {label} (torch.matmul) | {ms:.3f} | {tf:.0f} TFLOP/s | {tf / 2500:.0%} |")
+            print(lines[-1], flush=True)
+        del a, b, bt
     return lines
 
 
 def main() -> None:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("--only", choices=["layer", "rounding", "replay", "ceilings"])
+    p.add_argument("--only", choices=["layer", "rounding", "replay", "ceilings", "gemm"])
     args = p.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit("bench_baselines.py needs a GPU")
@@ -311,6 +323,9 @@ def main() -> None:
     if args.only in (None, "ceilings"):
         print("## Ceilings of this box\n", flush=True)
         ceilings_table(flush)
+    if args.only == "gemm":
+        print("## Dense GEMMs (hipBLASLt)\n", flush=True)
+        gemm_table(flush)
 
 
 if __name__ == "__main__":

@@ -60,6 +60,19 @@ template <int R, int BN, int WAVES, int STAGES>
 using ChunkCfg = DmaCfg<32 * R, BN, 32, STAGES, 1, WAVES, 0, 2, (WAVES == 8 && R >= 6) ? 4 : 5,
                         (32 * R * BN * 2 > 160 * 1024) ? 2 : 1, STAGES == 4 ? 1 : 0>;
 
+template <class T>
+struct Tag {
+  using type = T;
+};
+
+// The DSD's tiles: as ChunkCfg, except that with 8 waves an even number of
+// row groups is split between two rows of 4 waves (a 256 x 256 tile: 128 x
+// 64 per wave, where one row of 8 waves would read all 256 A rows in every
+// wave). At most 128 accumulators then, so always PIPE 5.
+template <int R, int BN, int WAVES, int STAGES>
+using DsdCfg = DmaCfg<32 * R, BN, 32, STAGES, (WAVES == 8 && R % 2 == 0) ? 2 : 1,
+                      (WAVES == 8 && R % 2 == 0) ? WAVES / 2 : WAVES, 0, 2, 5, 1, STAGES == 4 ? 1 : 0>;
+
 // LDS of the expert tiles of a kernel: the largest over its tile heights.
 template <int BN, int WAVES, int STAGES, int R>
 constexpr int chunk_lds_bytes() {
@@ -154,9 +167,10 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
   });
 }
 
-// Expert tiles of the DSD (defined below): 4 waves, 256 columns, chunks of up
-// to 256 rows. The SDD's choice follows the DSD's, so both are needed here.
-constexpr int kDsdBN = 256, kDsdWaves = 4, kDsdRmax = 8, kDsdStages = 4;
+// Expert tiles of the DSD (defined below): 256 columns, chunks of up to 256
+// rows, 4 waves (8 for a reduction of F >= 8192, as sb_dsd's row-block
+// tiles). The SDD's choice follows the DSD's, so both are needed here.
+constexpr int kDsdBN = 256, kDsdRmax = 8, kDsdStages = 4;
 
 // Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 192 rows;
 // tiles of up to 128 rows have a 4-stage ring (4 x 40 KB fits the 160 KB).
@@ -292,16 +306,16 @@ __device__ __forceinline__ void dsd_chunk_tile(uint8_t* __restrict__ lds, const 
 // code as the expert chunks (one H buffer, K steps through the row block's
 // own F/128 blocks, as the routing layout stores them).
 
-template <class CfgB>
-__global__ void __launch_bounds__(64 * kDsdWaves)
+template <class CfgB, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
     dsd_layer_kernel(const uint16_t* __restrict__ h, const uint16_t* __restrict__ w2,
                      const int32_t* __restrict__ tokens_per_expert, const int32_t* __restrict__ padded_offsets,
                      const int32_t* __restrict__ row_block_expert, uint16_t* __restrict__ out, int64_t h_bytes,
                      int32_t num_experts, int32_t ffn_dim, int32_t d_model, int32_t max_row_blocks, int32_t group,
                      int32_t force) {
-  static_assert(CfgB::kThreads == 64 * kDsdWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
+  static_assert(CfgB::kThreads == 64 * WAVES && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
   __shared__ __attribute__((aligned(1024)))
-  uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, kDsdWaves, kDsdStages, kDsdRmax>(), CfgB::kLdsAlloc)];
+  uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, WAVES, kDsdStages, kDsdRmax>(), CfgB::kLdsAlloc)];
   // As in the SDD: at most live row blocks x D/256 tiles either way.
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   if (static_cast<int>(blockIdx.x) >= live_rb * (d_model / kDsdBN)) return;
@@ -336,7 +350,7 @@ __global__ void __launch_bounds__(64 * kDsdWaves)
     return;
   with_groups<kDsdRmax>(ch.groups, [&](auto rc) {
     constexpr int R = decltype(rc)::value;
-    dsd_chunk_tile<ChunkCfg<R, kDsdBN, kDsdWaves, kDsdStages>>(lds, a, ch, slice * kDsdBN);
+    dsd_chunk_tile<DsdCfg<R, kDsdBN, WAVES, kDsdStages>>(lds, a, ch, slice * kDsdBN);
   });
 }
 
@@ -418,7 +432,7 @@ int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, 
                                        apply_gelu, force, stream);
 }
 
-template <class CfgB>
+template <class CfgB, int WAVES>
 int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
                      const int32_t* row_block_expert, void* out, int64_t max_row_blocks, int64_t num_experts,
                      int64_t num_copies, int64_t ffn_dim, int64_t d_model, int32_t force, hipStream_t stream) {
@@ -426,7 +440,7 @@ int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_ex
   int64_t tiles = 0;
   if (const int rc = dsd_layer_grid(max_row_blocks, num_experts, d_model, force, &tiles)) return rc;
   const int64_t h_bytes = max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2;
-  dsd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kDsdWaves, 0, stream>>>(
+  dsd_layer_kernel<CfgB, WAVES><<<static_cast<uint32_t>(tiles), 64 * WAVES, 0, stream>>>(
       static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w2), tokens_per_expert, padded_offsets,
       row_block_expert, static_cast<uint16_t*>(out), h_bytes, static_cast<int32_t>(num_experts),
       static_cast<int32_t>(ffn_dim), static_cast<int32_t>(d_model), static_cast<int32_t>(max_row_blocks),
@@ -511,14 +525,19 @@ extern "C" int sb_dsd_experts(const void* h, const void* w2, const int32_t* toke
     return sb_dsd(h, w2, row_offsets, col_indices, out, max_row_blocks * (ffn_dim / kBS), num_experts * ffn_dim,
                   max_row_blocks, kBS, d_model, 0, stream);
   const hipStream_t s = as_stream(stream);
-  // Row-block tile: sb_dsd's 128 x 512 tile of 4 waves (its tile for K < 8192);
-  // 128 x 256 when D % 512 != 0.
-  const int rc = d_model % 512 == 0
-                     ? launch_dsd_layer<ChunkCfg<4, 512, 4, 4>>(h, w2, tokens_per_expert, padded_offsets,
-                                                                row_block_expert, out, max_row_blocks, num_experts,
-                                                                num_copies, ffn_dim, d_model, force, s)
-                     : launch_dsd_layer<ChunkCfg<4, 256, 4, 4>>(h, w2, tokens_per_expert, padded_offsets,
-                                                                row_block_expert, out, max_row_blocks, num_experts,
-                                                                num_copies, ffn_dim, d_model, force, s);
+  // Row-block tile: sb_dsd's 128 x 512 tile (4 waves, or 8 for K >= 8192);
+  // 128 x 256 when D % 512 != 0. The expert tiles take the same wave count.
+  auto launch = [&](auto cfg, auto waves) {  // cfg: Tag<row-block config>
+    return launch_dsd_layer<typename decltype(cfg)::type, decltype(waves)::value>(
+        h, w2, tokens_per_expert, padded_offsets, row_block_expert, out, max_row_blocks, num_experts, num_copies,
+        ffn_dim, d_model, force, s);
+  };
+  using W4 = std::integral_constant<int, 4>;
+  using W8 = std::integral_constant<int, 8>;
+  const bool wide = d_model % 512 == 0, deep = ffn_dim >= 8192;
+  const int rc = wide ? (deep ? launch(Tag<DsdCfg<4, 512, 8, 4>>{}, W8{})
+                              : launch(Tag<DsdCfg<4, 512, 4, 4>>{}, W4{}))
+                      : (deep ? launch(Tag<DsdCfg<4, 256, 8, 4>>{}, W8{})
+                              : launch(Tag<DsdCfg<4, 256, 4, 4>>{}, W4{}));
   return rc ? rc : clear_ok();
 }

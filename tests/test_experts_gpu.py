@@ -56,6 +56,10 @@ CASES = {
     "uniform_wide": (lambda s: routing_case("random", 4096, 64, seed=1), 64, 256, 4096),
     # 1024 rows per expert: the SDD keeps row blocks, the DSD takes chunks.
     "few_experts": (lambda s: routing_case("random", 2048, 4, seed=s), 4, 256, 512),
+    # A reduction of F >= 8192: the DSD's 8-wave tiles (row blocks, and
+    # chunks of every row-group count: odd ones in one row of 8 waves, even
+    # ones split between two rows of 4).
+    "edges_deep": (lambda s: edge_routing(s), len(EDGE_COUNTS), 512, 8192),
 }
 
 # SDD-only cases (D % 256 != 0 leaves the DSD's layer tiles out): short
@@ -127,7 +131,7 @@ def test_sdd_experts_rows_equal_row_block_kernel(monkeypatch, gate: str, case: s
     pad = torch.as_tensor(chunk_pad_rows(topo, SDD_RMAX), device="cuda")
     if pad.numel():
         assert torch.all(h_ex[pad] == 0)
-    if case == "edges" or case in SDD_CASES:  # and against the oracle directly
+    if case.startswith("edges") or case in SDD_CASES:  # and against the oracle directly
         lay = build_layout(idx.numpy(), e, f, 128)
         ref = dense_rows(sdd_blocks(x.float(), w1.float(), lay), f // 128)
         live = rows[rows < ref.shape[0]].cpu()
@@ -151,7 +155,7 @@ def test_dsd_experts_rows_equal_row_block_kernel(monkeypatch, case: str, gate: s
     y_ex = _C.dsd_experts_cuda(h, w2_cat, topo)
     rows = torch.as_tensor(real_rows(topo), device="cuda")
     assert torch.equal(y_ex[rows], y_rb[rows])
-    if case == "edges":
+    if case.startswith("edges"):
         lay = build_layout(idx.numpy(), e, f, 128)
         ref = dsd_rows(h[: lay.col_indices.size].float().cpu(), w2_cat.float().cpu(), lay)
         live = rows[rows < ref.shape[0]].cpu()
@@ -186,7 +190,7 @@ def test_dsd_experts_padding_rows_do_not_reach_real_rows(monkeypatch, gate: str)
 
 
 @pytest.mark.parametrize("gate", GATES)
-@pytest.mark.parametrize("case", ["uniform64", "zipf130", "edges", "skewed"])
+@pytest.mark.parametrize("case", ["uniform64", "zipf130", "edges", "skewed", "edges_deep"])
 def test_moe_forward_expert_tiles_bit_identical(monkeypatch, case: str, gate: str) -> None:
     from sparsebench_amd.moe import moe_forward
 

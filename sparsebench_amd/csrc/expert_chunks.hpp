@@ -19,7 +19,7 @@ constexpr int kBS = 128;
 // Chunks of an expert with n real rows, for tiles of at most 32 * RMAX rows.
 template <int RMAX>
 struct Chunking {
-  static_assert(RMAX >= 4 && RMAX <= 8, "a tile holds one to two row blocks");
+  static_assert(RMAX >= 4 && RMAX <= 10, "a tile holds one to two row blocks and a 64-row piece");
   static constexpr int kRows = kBS * ((32 * RMAX) / kBS);  // rows of a full chunk
   static constexpr int kMerge = 32 * RMAX - kRows;         // a last piece up to this size joins the one before
   __device__ __forceinline__ static int count(int32_t n) {
@@ -144,13 +144,14 @@ struct LayoutSummary {
   int32_t chunks_a;  // chunks of up to 32 RA rows
   int32_t chunks_b;  // chunks of up to 32 RB rows
   int32_t chunks_c;  // chunks of up to 32 RC rows (0 when RC is 0)
+  int32_t chunks_d;  // chunks of up to 32 RD rows (0 when RD is 0)
 };
 
-template <int RA, int RB, int RC = 0>
+template <int RA, int RB, int RC = 0, int RD = 0>
 __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restrict__ tokens_per_expert,
                                                           int32_t num_experts) {
   int64_t rows = 0;
-  int32_t most = 0, ca = 0, cb = 0, cc = 0;
+  int32_t most = 0, ca = 0, cb = 0, cc = 0, cd = 0;
 #pragma unroll 1
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
@@ -160,6 +161,7 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
     ca += Chunking<RA>::count(v);
     cb += Chunking<RB>::count(v);
     if constexpr (RC > 0) cc += Chunking<RC>::count(v);
+    if constexpr (RD > 0) cd += Chunking<RD>::count(v);
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
@@ -168,6 +170,7 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
     ca += __shfl_xor(ca, d, 64);
     cb += __shfl_xor(cb, d, 64);
     if constexpr (RC > 0) cc += __shfl_xor(cc, d, 64);
+    if constexpr (RD > 0) cd += __shfl_xor(cd, d, 64);
   }
   LayoutSummary sum;
   sum.rows = rows;
@@ -175,6 +178,7 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
   sum.chunks_a = __builtin_amdgcn_readfirstlane(ca);
   sum.chunks_b = __builtin_amdgcn_readfirstlane(cb);
   sum.chunks_c = __builtin_amdgcn_readfirstlane(cc);
+  sum.chunks_d = __builtin_amdgcn_readfirstlane(cd);
   return sum;
 }
 

@@ -18,7 +18,11 @@
 //        one tile), 512 columns per tile, 8 waves of 64 columns.
 //   DSD  chunks of up to 256 rows (RMAX 8), 256 columns per tile, 4 waves
 //        of 64 columns; at the fine-grained shape 64 experts x 4 slices is
-//        one tile per CU.
+//        one tile per CU. For a reduction of F >= 8192, 8 waves and chunks
+//        of 256 rows whose last piece of up to 64 rows joins the chunk
+//        before it (RMAX 10): at the Mixtral-like shape every expert is then
+//        four chunks, 512 tiles in two rounds on 256 CUs, where a fifth,
+//        nearly empty chunk per expert made 592 tiles and a third round.
 // Rows of a chunk past its real rows are read as zeros (out-of-range DMA,
 // no memory read). SDD writes all 32 R rows of a chunk (padding rows as
 // GELU(0) = 0); DSD writes the real rows only. Padding rows past an
@@ -168,9 +172,14 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
 }
 
 // Expert tiles of the DSD (defined below): 256 columns, chunks of up to 256
-// rows, 4 waves (8 for a reduction of F >= 8192, as sb_dsd's row-block
-// tiles). The SDD's choice follows the DSD's, so both are needed here.
-constexpr int kDsdBN = 256, kDsdRmax = 8, kDsdStages = 4;
+// rows, 4 waves; for a reduction of F >= 8192, 8 waves (as sb_dsd's
+// row-block tiles) and a last piece of up to 64 rows joined to the chunk
+// before it (tiles of up to 320 rows; with 4 waves the 320 accumulators of
+// such a tile spill). The SDD's choice follows the DSD's, so both are
+// needed here.
+constexpr int kDsdBN = 256, kDsdStages = 4, kDsdDeepF = 8192;
+template <int WAVES>
+constexpr int dsd_rmax() { return WAVES == 8 ? 10 : 8; }
 
 // Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 192 rows;
 // tiles of up to 128 rows have a 4-stage ring (4 x 40 KB fits the 160 KB).
@@ -194,12 +203,15 @@ __global__ void __launch_bounds__(64 * kSddWaves)
   // blocks x slices tiles either way.
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   if (static_cast<int>(blockIdx.x) >= live_rb * (ffn_dim / kSddBN)) return;
-  const LayoutSummary sum = summarize_layout<kSddRmax, 4, kDsdRmax>(tokens_per_expert, num_experts);
+  const LayoutSummary sum =
+      summarize_layout<kSddRmax, 4, dsd_rmax<4>(), dsd_rmax<8>()>(tokens_per_expert, num_experts);
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
   // The DSD's own choice (dsd_layer_kernel): its expert tiles when the
   // routing is balanced and its grid of dsd_grid workgroups holds them all.
   const bool dsd_expert = force == 1 || (expert_stage_runs(sum, num_experts, kGateDsd, force) &&
-                                         static_cast<int64_t>(sum.chunks_c) * (d_model / kDsdBN) <= dsd_grid);
+                                         static_cast<int64_t>(ffn_dim >= kDsdDeepF ? sum.chunks_d : sum.chunks_c) *
+                                                 (d_model / kDsdBN) <=
+                                             dsd_grid);
   if (!(expert_stage_runs(sum, num_experts, kGateSdd, force) && dsd_expert)) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in
     // order; every row is computed and written (padding rows read as zeros).
@@ -314,12 +326,13 @@ __global__ void __launch_bounds__(64 * WAVES)
                      int32_t num_experts, int32_t ffn_dim, int32_t d_model, int32_t max_row_blocks, int32_t group,
                      int32_t force) {
   static_assert(CfgB::kThreads == 64 * WAVES && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
+  constexpr int kRmax = dsd_rmax<WAVES>();
   __shared__ __attribute__((aligned(1024)))
-  uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, WAVES, kDsdStages, kDsdRmax>(), CfgB::kLdsAlloc)];
+  uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, WAVES, kDsdStages, kRmax>(), CfgB::kLdsAlloc)];
   // As in the SDD: at most live row blocks x D/256 tiles either way.
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   if (static_cast<int>(blockIdx.x) >= live_rb * (d_model / kDsdBN)) return;
-  const LayoutSummary sum = summarize_layout<kDsdRmax, 4>(tokens_per_expert, num_experts);
+  const LayoutSummary sum = summarize_layout<kRmax, 4>(tokens_per_expert, num_experts);
   const DsdArgs a{h, w2, out, h_bytes, ffn_dim, d_model};
   // The grid may hold fewer workgroups than expert tiles (see the launch):
   // then the row blocks take the stage.
@@ -344,13 +357,18 @@ __global__ void __launch_bounds__(64 * WAVES)
   int c, slice;
   tile_coords(tile, chunks, slices, group, &c, &slice);
   if (c >= chunks) return;
-  const Chunk ch = find_chunk<kDsdRmax>(tokens_per_expert, padded_offsets, num_experts, c);
-  if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kDsdRmax ||
+  const Chunk ch = find_chunk<kRmax>(tokens_per_expert, padded_offsets, num_experts, c);
+  if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kRmax ||
       ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
     return;
-  with_groups<kDsdRmax>(ch.groups, [&](auto rc) {
+  // Nine row groups run as ten (the tenth reads zeros): in one row of 8
+  // waves, nine groups read 11 LDS fragments per 9 MFMAs against 9 per 10
+  // split between two rows of 4.
+  with_groups<kRmax>(ch.groups == 9 ? 10 : ch.groups, [&](auto rc) {
     constexpr int R = decltype(rc)::value;
-    dsd_chunk_tile<DsdCfg<R, kDsdBN, WAVES, kDsdStages>>(lds, a, ch, slice * kDsdBN);
+    if constexpr (R != 9) {
+      dsd_chunk_tile<DsdCfg<R, kDsdBN, WAVES, kDsdStages>>(lds, a, ch, slice * kDsdBN);
+    }
   });
 }
 
@@ -388,7 +406,9 @@ int dsd_layer_grid(int64_t max_row_blocks, int64_t num_experts, int64_t d_model,
   if (const int rc = device_cus(&cus)) return rc;
   const int64_t rows = std::min(max_row_blocks * kBS, std::max<int64_t>(0, max_row_blocks * kBS - (kBS - 1) * num_experts) +
                                                           (kBS - 1));
-  const int64_t chunk_bound = std::min(max_row_blocks, std::min(num_experts, rows) + rows / (32 * kDsdRmax));
+  const int64_t chunk_bound =
+      std::min(max_row_blocks, std::min(num_experts, rows) + rows / Chunking<dsd_rmax<4>()>::kRows);
+  static_assert(Chunking<dsd_rmax<4>()>::kRows == Chunking<dsd_rmax<8>()>::kRows, "one bound for both");
   const int64_t expert_tiles = chunk_bound * (d_model / kDsdBN);
   const int64_t forced_expert = force == 1 ? expert_tiles : 0;
   const int64_t rb_bn = d_model % 512 == 0 ? 512 : 256;
@@ -534,7 +554,7 @@ extern "C" int sb_dsd_experts(const void* h, const void* w2, const int32_t* toke
   };
   using W4 = std::integral_constant<int, 4>;
   using W8 = std::integral_constant<int, 8>;
-  const bool wide = d_model % 512 == 0, deep = ffn_dim >= 8192;
+  const bool wide = d_model % 512 == 0, deep = ffn_dim >= kDsdDeepF;
   const int rc = wide ? (deep ? launch(Tag<DsdCfg<4, 512, 8, 4>>{}, W8{})
                               : launch(Tag<DsdCfg<4, 512, 4, 4>>{}, W4{}))
                       : (deep ? launch(Tag<DsdCfg<4, 256, 8, 4>>{}, W8{})

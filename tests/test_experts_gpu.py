@@ -56,6 +56,10 @@ CASES = {
     "uniform_wide": (lambda s: routing_case("random", 4096, 64, seed=1), 64, 256, 4096),
     # 1024 rows per expert: the SDD keeps row blocks, the DSD takes chunks.
     "few_experts": (lambda s: routing_case("random", 2048, 4, seed=s), 4, 256, 512),
+    # The Mixtral-like shape's routing (971-1057 rows per expert with seed 0)
+    # with F >= 8192: the DSD's 8-wave expert tiles join a last piece of up
+    # to 64 rows to the chunk before it (tiles of 9 and 10 row groups).
+    "big_experts": (lambda s: routing_case("random", 4096, 8, seed=0), 8, 256, 8192),
     # A reduction of F >= 8192: the DSD's 8-wave tiles (row blocks, and
     # chunks of every row-group count: odd ones in one row of 8 waves, even
     # ones split between two rows of 4).
@@ -265,12 +269,22 @@ def dsd_grid(max_rb: int, e: int, d: int) -> int:
     return max(min(chunk_bound * (d // 256), 4 * 256), max_rb * (d // (512 if d % 512 == 0 else 256)))
 
 
-def dsd_chunks(counts: list[int]) -> int:
-    """Chunks of up to 256 rows (the DSD's expert tiles)."""
-    return sum(-(-c // 256) for c in counts if c > 0)
+def chunk_count(n: int, rows: int, merge: int) -> int:
+    """Chunks of an expert with n rows: `rows` each, a last piece of up to `merge` rows joined to the one before."""
+    if n <= 0:
+        return 0
+    c = -(-n // rows)
+    return c - (1 if c >= 2 and n - rows * (c - 1) <= merge else 0)
 
 
-def gate_rule(counts: list[int], stage: str, max_rb: int, d: int) -> bool:
+def dsd_chunks(counts: list[int], f: int) -> int:
+    """Chunks of the DSD's expert tiles: 256 rows, and for F >= 8192 (8 waves)
+    a last piece of up to 64 rows joined to the chunk before it."""
+    merge = 64 if f >= 8192 else 0
+    return sum(chunk_count(c, 256, merge) for c in counts)
+
+
+def gate_rule(counts: list[int], stage: str, max_rb: int, d: int, f: int) -> bool:
     """The choice stated in expert_chunks.hpp, restated: the DSD takes expert
     tiles iff no expert holds more than twice the mean rows and its grid
     holds all of them; the SDD iff, besides, the mean is at most 256 rows
@@ -278,7 +292,7 @@ def gate_rule(counts: list[int], stage: str, max_rb: int, d: int) -> bool:
     counts = [max(c, 0) for c in counts]
     total, most, e = sum(counts), max(counts), len(counts)
     balanced = total > 0 and most * e <= 2 * total
-    dsd = balanced and dsd_chunks(counts) * (d // 256) <= dsd_grid(max_rb, e, d)
+    dsd = balanced and dsd_chunks(counts, f) * (d // 256) <= dsd_grid(max_rb, e, d)
     return dsd and (stage == "dsd" or total <= 256 * e)
 
 
@@ -318,10 +332,10 @@ def test_device_choice_follows_the_rule(case: str) -> None:
     dense = dense_rows(h, fb)
     if f % 512 == 0 and untouched:
         sdd_expert = bool(torch.isnan(dense[torch.tensor(untouched, device="cuda")]).all())
-        assert sdd_expert == gate_rule(counts, "sdd", max_rb, d)
+        assert sdd_expert == gate_rule(counts, "sdd", max_rb, d, f)
     if pad:
         dsd_expert = bool(torch.isnan(y[torch.tensor(pad, device="cuda")]).all())
-        assert dsd_expert == gate_rule(counts, "dsd", max_rb, d)
+        assert dsd_expert == gate_rule(counts, "dsd", max_rb, d, f)
 
 
 def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(monkeypatch) -> None:
@@ -345,8 +359,8 @@ def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(mon
     topo = route_device(idx, e, f, 128)
     max_rb = topo.row_token.numel() // 128
     counts = topo.tokens_per_expert.cpu().tolist()
-    assert dsd_chunks(counts) * (d // 256) > dsd_grid(max_rb, e, d)
-    assert not gate_rule(counts, "sdd", max_rb, d) and not gate_rule(counts, "dsd", max_rb, d)
+    assert dsd_chunks(counts, f) * (d // 256) > dsd_grid(max_rb, e, d)
+    assert not gate_rule(counts, "sdd", max_rb, d, f) and not gate_rule(counts, "dsd", max_rb, d, f)
     monkeypatch.delenv("SPARSEBENCH_EXPERT_GATE", raising=False)
     fb = f // 128
     h = torch.full((max_rb * fb, 128, 128), float("nan"), dtype=torch.bfloat16, device="cuda")

@@ -82,6 +82,43 @@ __device__ __forceinline__ int xcd_remap(int bid, int live) {
   return x < rem ? x * (per + 1) + q : rem * (per + 1) + (x - rem) * per + q;
 }
 
+// The same spread, with a short last round split. An XCD that runs n of the
+// tiles on c CUs runs them in ceil(n / c) rounds; when its last round holds
+// r <= c / 2 tiles, those r tiles are each split into two column halves that
+// run as workgroups of their own, so 2r CUs share the round and it ends
+// sooner (a half tile takes a little over half the time of a whole one).
+// Workgroup bid gets logical tile `tile` (>= tiles: no work) and `half`:
+// -1 for the whole tile, else 0 or 1. The grid needs up to
+// kNumXcd * (ceil(tiles / kNumXcd) + c / 2) workgroups; ids past an XCD's
+// share get tile = tiles.
+struct TailTile {
+  int tile, half;
+};
+__device__ __forceinline__ TailTile split_tail(int bid, int tiles, int cus_per_xcd) {
+  const int per = tiles / kNumXcd;
+  const int rem = tiles % kNumXcd;
+  const int x = bid % kNumXcd;
+  const int q = bid / kNumXcd;
+  const int n = per + (x < rem ? 1 : 0);
+  const int start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+  const int r = cus_per_xcd > 0 ? n % cus_per_xcd : 0;
+  const int split = (r > 0 && 2 * r <= cus_per_xcd) ? r : 0;
+  const int whole = n - split;
+  TailTile t{tiles, -1};
+  if (q < whole) {
+    t.tile = start + q;
+  } else if (q < whole + 2 * split) {
+    t.tile = start + whole + (q - whole) / 2;
+    t.half = (q - whole) % 2;
+  }
+  t.tile = __builtin_amdgcn_readfirstlane(t.tile);
+  t.half = __builtin_amdgcn_readfirstlane(t.half);
+  return t;
+}
+
+// Extra workgroups a grid of split_tail needs beyond its tiles.
+inline int64_t split_tail_slack(int cus) { return kNumXcd * (cus / kNumXcd / 2 + 1); }
+
 // Logical tile -> (row block, column slice) for the live region: tiles are
 // taken in groups of `group` row blocks, walking down the group one column
 // slice at a time, so the tiles that run together on one XCD cover a few

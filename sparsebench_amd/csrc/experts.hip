@@ -192,17 +192,20 @@ __global__ void __launch_bounds__(64 * kSddWaves)
                      const int32_t* __restrict__ row_offsets, const int32_t* __restrict__ tokens_per_expert,
                      const int32_t* __restrict__ padded_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
                      int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t max_row_blocks,
-                     int32_t apply_gelu, int32_t group, int32_t force, int32_t dsd_grid) {
+                     int32_t apply_gelu, int32_t group, int32_t force, int32_t dsd_grid, int32_t cus_per_xcd,
+                     int32_t tail_slack) {
   static_assert(CfgB::kThreads == 64 * kSddWaves && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
+  using CfgH = SddHalfTile;
+  static_assert(CfgH::kThreads == CfgB::kThreads && 2 * CfgH::BN == CfgB::BN, "half tiles: same workgroup");
   __shared__ __attribute__((aligned(1024)))
   uint8_t lds[max_int(max_int(chunk_lds_bytes<kSddBN, kSddWaves, kSddStages, kSddRmax>(),
                                chunk_lds_bytes<kSddBN, kSddWaves, 4, 4>()),
-                       CfgB::kLdsAlloc)];
+                       max_int(CfgB::kLdsAlloc, CfgH::kLdsAlloc))];
   // Workgroups past both tilings' tiles leave before the summary: every
   // chunk starts a row block of its own, so there are at most live row
   // blocks x slices tiles either way.
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
-  if (static_cast<int>(blockIdx.x) >= live_rb * (ffn_dim / kSddBN)) return;
+  if (static_cast<int>(blockIdx.x) >= live_rb * (ffn_dim / kSddBN) + tail_slack) return;
   const LayoutSummary sum =
       summarize_layout<kSddRmax, 4, dsd_rmax<4>(), dsd_rmax<8>()>(tokens_per_expert, num_experts);
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
@@ -215,15 +218,21 @@ __global__ void __launch_bounds__(64 * kSddWaves)
   if (!(expert_stage_runs(sum, num_experts, kGateSdd, force) && dsd_expert)) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in
     // order; every row is computed and written (padding rows read as zeros).
+    // The tiles of a short last round run as column halves (split_tail).
     const int blocks = sum.chunks_b;
     const int slices = ffn_dim / CfgB::BN;
-    const int tile = xcd_remap(static_cast<int>(blockIdx.x), blocks * slices);
+    const TailTile tt = split_tail(static_cast<int>(blockIdx.x), blocks * slices, cus_per_xcd);
+    if (tt.tile >= blocks * slices) return;
     int rb, slice;
-    tile_coords(tile, blocks, slices, group, &rb, &slice);
+    tile_coords(tt.tile, blocks, slices, group, &rb, &slice);
     if (rb >= blocks || rb >= max_row_blocks) return;
     const int32_t expert = __builtin_amdgcn_readfirstlane(row_block_expert[rb]);
     if (expert < 0 || expert >= num_experts) return;
-    sdd_chunk_tile<CfgB>(lds, a, Chunk{expert, rb * kBS, kBS, 4}, slice * CfgB::BN);
+    const Chunk ch{expert, rb * kBS, kBS, 4};
+    if (tt.half < 0)
+      sdd_chunk_tile<CfgB>(lds, a, ch, slice * CfgB::BN);
+    else
+      sdd_chunk_tile<CfgH>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
     return;
   }
   const int chunks = sum.chunks_a;
@@ -324,31 +333,38 @@ __global__ void __launch_bounds__(64 * WAVES)
                      const int32_t* __restrict__ tokens_per_expert, const int32_t* __restrict__ padded_offsets,
                      const int32_t* __restrict__ row_block_expert, uint16_t* __restrict__ out, int64_t h_bytes,
                      int32_t num_experts, int32_t ffn_dim, int32_t d_model, int32_t max_row_blocks, int32_t group,
-                     int32_t force) {
+                     int32_t force, int32_t tile_grid, int32_t cus_per_xcd, int32_t tail_slack) {
   static_assert(CfgB::kThreads == 64 * WAVES && CfgB::BM == kBS, "row-block tiles: 128 rows, same workgroup");
+  using CfgH = DsdCfg<4, CfgB::BN / 2, WAVES, kDsdStages>;
   constexpr int kRmax = dsd_rmax<WAVES>();
   __shared__ __attribute__((aligned(1024)))
-  uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, WAVES, kDsdStages, kRmax>(), CfgB::kLdsAlloc)];
-  // As in the SDD: at most live row blocks x D/256 tiles either way.
+  uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, WAVES, kDsdStages, kRmax>(), max_int(CfgB::kLdsAlloc, CfgH::kLdsAlloc))];
+  // As in the SDD: at most live row blocks x D/256 tiles either way, plus
+  // the split halves of a short last round.
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
-  if (static_cast<int>(blockIdx.x) >= live_rb * (d_model / kDsdBN)) return;
+  if (static_cast<int>(blockIdx.x) >= live_rb * (d_model / kDsdBN) + tail_slack) return;
   const LayoutSummary sum = summarize_layout<kRmax, 4>(tokens_per_expert, num_experts);
   const DsdArgs a{h, w2, out, h_bytes, ffn_dim, d_model};
   // The grid may hold fewer workgroups than expert tiles (see the launch):
   // then the row blocks take the stage.
-  const bool fits = static_cast<int64_t>(sum.chunks_a) * (d_model / kDsdBN) <= static_cast<int64_t>(gridDim.x);
+  const bool fits = static_cast<int64_t>(sum.chunks_a) * (d_model / kDsdBN) <= static_cast<int64_t>(tile_grid);
   if (!(expert_stage_runs(sum, num_experts, kGateDsd, force) && (fits || force == 1))) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in order.
+    // The tiles of a short last round run as column halves (split_tail).
     const int blocks = sum.chunks_b;
     const int slices = d_model / CfgB::BN;
-    const int tile = xcd_remap(static_cast<int>(blockIdx.x), blocks * slices);
+    const TailTile tt = split_tail(static_cast<int>(blockIdx.x), blocks * slices, cus_per_xcd);
+    if (tt.tile >= blocks * slices) return;
     int rb, slice;
-    tile_coords(tile, blocks, slices, group, &rb, &slice);
+    tile_coords(tt.tile, blocks, slices, group, &rb, &slice);
     if (rb >= blocks || rb >= max_row_blocks) return;
     const int32_t expert = __builtin_amdgcn_readfirstlane(row_block_expert[rb]);
     if (expert < 0 || expert >= num_experts) return;
     const Chunk ch{expert, rb * kBS, kBS, 4};
-    dsd_chunk_tile<CfgB>(lds, a, ch, slice * CfgB::BN);
+    if (tt.half < 0)
+      dsd_chunk_tile<CfgB>(lds, a, ch, slice * CfgB::BN);
+    else
+      dsd_chunk_tile<CfgH>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
     return;
   }
   const int chunks = sum.chunks_a;
@@ -429,12 +445,15 @@ int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, co
   int64_t dsd_grid = 0;  // no DSD expert tiles for D % 256 != 0
   if (d_model % kDsdBN == 0)
     if (const int rc = dsd_layer_grid(max_row_blocks, num_experts, d_model, force, &dsd_grid)) return rc;
-  sdd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles), 64 * kSddWaves, 0, stream>>>(
+  int cus = 0;
+  if (const int rc = device_cus(&cus)) return rc;
+  const int64_t slack = split_tail_slack(cus);
+  sdd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles + slack), 64 * kSddWaves, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
       tokens_per_expert, padded_offsets, static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens),
       static_cast<int32_t>(d_model), static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts),
       static_cast<int32_t>(max_row_blocks), apply_gelu, kTileGroup, force,
-      static_cast<int32_t>(std::min<int64_t>(dsd_grid, 2147483647)));
+      static_cast<int32_t>(std::min<int64_t>(dsd_grid, 2147483647)), cus / kNumXcd, static_cast<int32_t>(slack));
   return check_launch("sdd_experts");
 }
 
@@ -460,11 +479,14 @@ int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_ex
   int64_t tiles = 0;
   if (const int rc = dsd_layer_grid(max_row_blocks, num_experts, d_model, force, &tiles)) return rc;
   const int64_t h_bytes = max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2;
-  dsd_layer_kernel<CfgB, WAVES><<<static_cast<uint32_t>(tiles), 64 * WAVES, 0, stream>>>(
+  int cus = 0;
+  if (const int rc = device_cus(&cus)) return rc;
+  const int64_t slack = split_tail_slack(cus);
+  dsd_layer_kernel<CfgB, WAVES><<<static_cast<uint32_t>(tiles + slack), 64 * WAVES, 0, stream>>>(
       static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w2), tokens_per_expert, padded_offsets,
       row_block_expert, static_cast<uint16_t*>(out), h_bytes, static_cast<int32_t>(num_experts),
       static_cast<int32_t>(ffn_dim), static_cast<int32_t>(d_model), static_cast<int32_t>(max_row_blocks),
-      kTileGroup, force);
+      kTileGroup, force, static_cast<int32_t>(tiles), cus / kNumXcd, static_cast<int32_t>(slack));
   return check_launch("dsd_experts");
 }
 
@@ -491,7 +513,8 @@ extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_
     return fail(SB_ERR_INVALID, "sdd needs F (%lld) to be a multiple of 256", static_cast<long long>(ffn_dim));
   if (num_tokens <= 0 || num_tokens > kI32Max || num_experts <= 0 || num_experts > kMaxExperts)
     return fail(SB_ERR_INVALID, "sdd_experts: bad token or expert count");
-  if (ffn_dim * d_model > kI32Max || max_row_blocks * kBS > kI32Max || max_row_blocks * (ffn_dim / kBS) > kI32Max)
+  if (ffn_dim * d_model > kI32Max || max_row_blocks * kBS > kI32Max ||
+      max_row_blocks * (ffn_dim / kBS) > kI32Max - 65536)
     return fail(SB_ERR_INVALID, "problem too large");
   const int32_t force = expert_gate_override();
   // The expert tiles are 512 wide; other widths take the per-row-block kernel.
@@ -537,7 +560,7 @@ extern "C" int sb_dsd_experts(const void* h, const void* w2, const int32_t* toke
   if (max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2 >= (int64_t{1} << 31) ||
       ffn_dim * d_model * 2 >= (int64_t{1} << 31))
     return fail(SB_ERR_INVALID, "dsd_experts: H or one expert's W2 too large for 32-bit buffer offsets");
-  if (max_row_blocks * kBS * d_model > (int64_t{1} << 62) || max_row_blocks * (d_model / kDsdBN) > kI32Max)
+  if (max_row_blocks * kBS * d_model > (int64_t{1} << 62) || max_row_blocks * (d_model / kDsdBN) > kI32Max - 65536)
     return fail(SB_ERR_INVALID, "problem too large");
   const int32_t force = expert_gate_override();
   // Row blocks forced: exactly sb_dsd version 5 (its default tile).

@@ -56,6 +56,10 @@ CASES = {
     "uniform_wide": (lambda s: routing_case("random", 4096, 64, seed=1), 64, 256, 4096),
     # 1024 rows per expert: the SDD keeps row blocks, the DSD takes chunks.
     "few_experts": (lambda s: routing_case("random", 2048, 4, seed=s), 4, 256, 512),
+    # Skewed routing with F % 512 == 0: both layer kernels run row blocks,
+    # fewer than one round of them, so each XCD's short round runs as
+    # column halves.
+    "zipf_rows": (lambda s: routing_case("zipf_perm", 2000, 32, seed=s), 32, 512, 1024),
     # The Mixtral-like shape's routing (971-1057 rows per expert with seed 0)
     # with F >= 8192: the DSD's 8-wave expert tiles join a last piece of up
     # to 64 rows to the chunk before it (tiles of 9 and 10 row groups).

@@ -112,6 +112,107 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
   return ch;
 }
 
+// Chunks by row-group count. An expert with n rows has c = count(n) chunks:
+// c - 1 full ones of kRows / 32 groups and a last one of
+// ceil((n - kRows (c - 1)) / 32) groups (up to RMAX with a joined piece).
+template <int RMAX>
+struct ChunkSizes {
+  static constexpr int kFull = Chunking<RMAX>::kRows / 32;
+  // Chunks of this expert with exactly g groups.
+  __device__ __forceinline__ static int with_groups(int32_t n, int g) {
+    const int c = Chunking<RMAX>::count(n);
+    if (c == 0) return 0;
+    const int last = (n - Chunking<RMAX>::kRows * (c - 1) + 31) / 32;
+    return (g == kFull ? c - 1 : 0) + (g == last ? 1 : 0);
+  }
+};
+
+// hist[g] = chunks of g row groups over all experts, g = 1 .. RMAX (every
+// wave computes the same values).
+template <int RMAX>
+__device__ __forceinline__ void chunk_group_hist(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
+                                                 int32_t (&hist)[RMAX + 1]) {
+  int32_t h[RMAX + 1] = {};
+#pragma unroll 1
+  for (int base = 0; base < num_experts; base += 64) {
+    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+#pragma unroll
+    for (int g = 1; g <= RMAX; ++g) h[g] += ChunkSizes<RMAX>::with_groups(n > 0 ? n : 0, g);
+  }
+#pragma unroll
+  for (int g = 1; g <= RMAX; ++g) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) h[g] += __shfl_xor(h[g], d, 64);
+    hist[g] = __builtin_amdgcn_readfirstlane(h[g]);
+  }
+  hist[0] = 0;
+}
+
+// Chunk k (0 <= k < the number of chunks) in size order: by row-group count,
+// largest first, and in expert order within one count (an expert's full
+// chunks before its last one), so the k-th chunk of that order and the
+// chunks of find_chunk are the same set.
+template <int RMAX>
+__device__ __forceinline__ Chunk find_chunk_by_size(const int32_t* __restrict__ tokens_per_expert,
+                                                    const int32_t* __restrict__ padded_offsets, int32_t num_experts,
+                                                    int k, const int32_t (&hist)[RMAX + 1]) {
+  Chunk ch{-1, 0, 0, 0};
+  int g = RMAX;
+  for (; g >= 1; --g) {  // the count that holds rank k, and k's rank within it
+    if (k < hist[g]) break;
+    k -= hist[g];
+  }
+  if (g < 1) return ch;
+  int before = 0;  // chunks of g groups of the experts before this pass
+  for (int base = 0; base < num_experts; base += 64) {
+    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int m = ChunkSizes<RMAX>::with_groups(n > 0 ? n : 0, g);
+    const int incl = wave_inclusive_scan(m);
+    const uint64_t reach = __ballot(before + incl > k);
+    if (reach != 0) {
+      const int l = __builtin_ctzll(reach);
+      const int i = k - (before + __shfl(incl - m, l, 64));
+      const int32_t n_e = __shfl(n, l, 64);
+      const int count = Chunking<RMAX>::count(n_e);
+      // The expert's chunks of g groups are its first m (all full ones, g
+      // = kFull) or its last one.
+      const int idx = g == ChunkSizes<RMAX>::kFull ? i : count - 1;
+      const int start = Chunking<RMAX>::kRows * idx;
+      ch.expert = base + l;
+      ch.row0 = padded_offsets[base + l] + start;
+      ch.rows = idx + 1 < count ? Chunking<RMAX>::kRows : n_e - start;
+      ch.groups = (ch.rows + 31) / 32;
+      break;
+    }
+    before += __shfl(incl, 63, 64);
+  }
+  ch.expert = __builtin_amdgcn_readfirstlane(ch.expert);
+  ch.row0 = __builtin_amdgcn_readfirstlane(ch.row0);
+  ch.rows = __builtin_amdgcn_readfirstlane(ch.rows);
+  ch.groups = __builtin_amdgcn_readfirstlane(ch.groups);
+  return ch;
+}
+
+// The XCD-balanced tile of workgroup bid over `chunks` chunks x `slices`
+// column slices. The chunks in size order are dealt to the XCDs like cards
+// in snake order (ranks 0-7 to XCDs 0-7, ranks 8-15 to XCDs 7-0, ...), so
+// each XCD gets a like mix of large and small tiles; an XCD runs its chunks
+// slice by slice, largest first, so the tiles dispatched last to the CUs
+// that free up first are the smallest. Workgroups are handed to the XCDs
+// round-robin by id. Returns false past the XCD's tiles (the grid needs up
+// to kNumXcd x ceil(chunks / kNumXcd) x slices workgroups).
+__device__ __forceinline__ bool balanced_chunk_tile(int bid, int chunks, int slices, int* rank, int* slice) {
+  const int x = bid % kNumXcd, q = bid / kNumXcd;
+  const int rows = chunks / kNumXcd, rem = chunks % kNumXcd;
+  const int pos = (rows & 1) ? kNumXcd - 1 - x : x;  // x's place in the partial row
+  const int n = rows + (pos < rem ? 1 : 0);           // chunks of XCD x
+  if (n == 0 || q >= n * slices) return false;
+  const int j = q % n;
+  *slice = __builtin_amdgcn_readfirstlane(q / n);
+  *rank = __builtin_amdgcn_readfirstlane(kNumXcd * j + ((j & 1) ? kNumXcd - 1 - x : x));
+  return true;
+}
+
 // Which tiling computes a stage of the MoE layer: expert chunks or row
 // blocks. Every workgroup of the stage's kernel makes the same choice from
 // the same counts, so it costs no host sync.
@@ -145,19 +246,21 @@ struct LayoutSummary {
   int32_t chunks_b;  // chunks of up to 32 RB rows
   int32_t chunks_c;  // chunks of up to 32 RC rows (0 when RC is 0)
   int32_t chunks_d;  // chunks of up to 32 RD rows (0 when RD is 0)
+  int32_t active;    // experts with at least one row
 };
 
 template <int RA, int RB, int RC = 0, int RD = 0>
 __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restrict__ tokens_per_expert,
                                                           int32_t num_experts) {
   int64_t rows = 0;
-  int32_t most = 0, ca = 0, cb = 0, cc = 0, cd = 0;
+  int32_t most = 0, ca = 0, cb = 0, cc = 0, cd = 0, act = 0;
 #pragma unroll 1
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
     const int32_t v = n > 0 ? n : 0;
     rows += v;
     most = max(most, v);
+    act += v > 0 ? 1 : 0;
     ca += Chunking<RA>::count(v);
     cb += Chunking<RB>::count(v);
     if constexpr (RC > 0) cc += Chunking<RC>::count(v);
@@ -171,6 +274,7 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
     cb += __shfl_xor(cb, d, 64);
     if constexpr (RC > 0) cc += __shfl_xor(cc, d, 64);
     if constexpr (RD > 0) cd += __shfl_xor(cd, d, 64);
+    act += __shfl_xor(act, d, 64);
   }
   LayoutSummary sum;
   sum.rows = rows;
@@ -179,6 +283,7 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
   sum.chunks_b = __builtin_amdgcn_readfirstlane(cb);
   sum.chunks_c = __builtin_amdgcn_readfirstlane(cc);
   sum.chunks_d = __builtin_amdgcn_readfirstlane(cd);
+  sum.active = __builtin_amdgcn_readfirstlane(act);
   return sum;
 }
 

@@ -203,9 +203,10 @@ __global__ void __launch_bounds__(64 * kSddWaves)
                        max_int(CfgB::kLdsAlloc, CfgH::kLdsAlloc))];
   // Workgroups past both tilings' tiles leave before the summary: every
   // chunk starts a row block of its own, so there are at most live row
-  // blocks x slices tiles either way.
+  // blocks x slices tiles either way, numbered up to kNumXcd - 1 chunk rows
+  // past them by the XCD deal, plus the split halves of a short last round.
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
-  if (static_cast<int>(blockIdx.x) >= live_rb * (ffn_dim / kSddBN) + tail_slack) return;
+  if (static_cast<int>(blockIdx.x) >= (live_rb + kNumXcd) * (ffn_dim / kSddBN) + tail_slack) return;
   const LayoutSummary sum =
       summarize_layout<kSddRmax, 4, dsd_rmax<4>(), dsd_rmax<8>()>(tokens_per_expert, num_experts);
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
@@ -235,20 +236,36 @@ __global__ void __launch_bounds__(64 * kSddWaves)
       sdd_chunk_tile<CfgH>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
     return;
   }
+  // Expert tiles. When every expert is one chunk, the chunks are dealt to
+  // the XCDs largest first (balanced_chunk_tile); an expert of several
+  // chunks keeps them on one XCD, where they share its W1 columns in L2
+  // (xcd_remap and groups of chunks x slices).
   const int chunks = sum.chunks_a;
   const int slices = ffn_dim / kSddBN;
-  const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);
-  int c, slice;
-  tile_coords(tile, chunks, slices, group, &c, &slice);
-  if (c >= chunks) return;
-  const Chunk ch = find_chunk<kSddRmax>(tokens_per_expert, padded_offsets, num_experts, c);
+  Chunk ch;
+  int n0_slice = 0;
+  if (chunks == sum.active) {
+    int rank, slice;
+    if (!balanced_chunk_tile(static_cast<int>(blockIdx.x), chunks, slices, &rank, &slice)) return;
+    int32_t hist[kSddRmax + 1];
+    chunk_group_hist<kSddRmax>(tokens_per_expert, num_experts, hist);
+    ch = find_chunk_by_size<kSddRmax>(tokens_per_expert, padded_offsets, num_experts, rank, hist);
+    n0_slice = slice;
+  } else {
+    const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);
+    int c, slice;
+    tile_coords(tile, chunks, slices, group, &c, &slice);
+    if (c >= chunks) return;
+    ch = find_chunk<kSddRmax>(tokens_per_expert, padded_offsets, num_experts, c);
+    n0_slice = slice;
+  }
   // Not a routing layout (the chunk would leave the buffers): skip it.
   if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kSddRmax ||
       ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
     return;
   with_groups<kSddRmax>(ch.groups, [&](auto rc) {
     constexpr int R = decltype(rc)::value;
-    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, (R <= 4 ? 4 : kSddStages)>>(lds, a, ch, slice * kSddBN);
+    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, (R <= 4 ? 4 : kSddStages)>>(lds, a, ch, n0_slice * kSddBN);
   });
 }
 
@@ -447,7 +464,7 @@ int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, co
     if (const int rc = dsd_layer_grid(max_row_blocks, num_experts, d_model, force, &dsd_grid)) return rc;
   int cus = 0;
   if (const int rc = device_cus(&cus)) return rc;
-  const int64_t slack = split_tail_slack(cus);
+  const int64_t slack = split_tail_slack(cus) + kNumXcd * (ffn_dim / kSddBN);
   sdd_layer_kernel<CfgB><<<static_cast<uint32_t>(tiles + slack), 64 * kSddWaves, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, row_block_expert, row_offsets,
       tokens_per_expert, padded_offsets, static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens),
@@ -514,7 +531,7 @@ extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_
   if (num_tokens <= 0 || num_tokens > kI32Max || num_experts <= 0 || num_experts > kMaxExperts)
     return fail(SB_ERR_INVALID, "sdd_experts: bad token or expert count");
   if (ffn_dim * d_model > kI32Max || max_row_blocks * kBS > kI32Max ||
-      max_row_blocks * (ffn_dim / kBS) > kI32Max - 65536)
+      (max_row_blocks + kNumXcd) * (ffn_dim / kBS) > kI32Max - 65536)
     return fail(SB_ERR_INVALID, "problem too large");
   const int32_t force = expert_gate_override();
   // The expert tiles are 512 wide; other widths take the per-row-block kernel.

@@ -80,16 +80,24 @@ struct Chunk {
   int32_t groups;  // 32-row groups of the tile
 };
 
-// Chunk c (0 <= c < the number of chunks) in expert order.
+// Padded rows of an expert with n real rows (the routing layout pads each
+// expert to whole row blocks).
+__device__ __forceinline__ int32_t padded_rows(int32_t n) { return n > 0 ? (n + kBS - 1) / kBS * kBS : 0; }
+
+// Chunk c (0 <= c < the number of chunks) in expert order. Its first row is
+// the expert's first padded row, the sum of the padded rows of the experts
+// before it (padded_offsets[e] of the routing layout), computed here from the
+// counts instead of loaded: one dependent load less before the tile's first.
 template <int RMAX>
-__device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_per_expert,
-                                            const int32_t* __restrict__ padded_offsets, int32_t num_experts, int c) {
+__device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts, int c) {
   Chunk ch{-1, 0, 0, 0};
-  int before = 0;  // chunks of the experts before this pass
+  int before = 0;       // chunks of the experts before this pass
+  int rows_before = 0;  // padded rows of the experts before this pass
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
     const int cc = Chunking<RMAX>::count(n);
     const int incl = wave_inclusive_scan(cc);
+    const int pincl = wave_inclusive_scan(padded_rows(n));
     const uint64_t reach = __ballot(before + incl > c);  // experts whose chunks run past c
     if (reach != 0) {
       const int l = __builtin_ctzll(reach);  // the first of them holds chunk c
@@ -98,12 +106,13 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
       const int32_t n_e = __shfl(n, l, 64);
       const int start = Chunking<RMAX>::kRows * i;
       ch.expert = base + l;
-      ch.row0 = padded_offsets[base + l] + start;
+      ch.row0 = rows_before + __shfl(pincl - padded_rows(n), l, 64) + start;
       ch.rows = i + 1 < count ? Chunking<RMAX>::kRows : n_e - start;
       ch.groups = (ch.rows + 31) / 32;
       break;
     }
     before += __shfl(incl, 63, 64);
+    rows_before += __shfl(pincl, 63, 64);
   }
   ch.expert = __builtin_amdgcn_readfirstlane(ch.expert);
   ch.row0 = __builtin_amdgcn_readfirstlane(ch.row0);
@@ -153,8 +162,7 @@ __device__ __forceinline__ void chunk_group_hist(const int32_t* __restrict__ tok
 // chunks before its last one), so the k-th chunk of that order and the
 // chunks of find_chunk are the same set.
 template <int RMAX>
-__device__ __forceinline__ Chunk find_chunk_by_size(const int32_t* __restrict__ tokens_per_expert,
-                                                    const int32_t* __restrict__ padded_offsets, int32_t num_experts,
+__device__ __forceinline__ Chunk find_chunk_by_size(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
                                                     int k, const int32_t (&hist)[RMAX + 1]) {
   Chunk ch{-1, 0, 0, 0};
   int g = RMAX;
@@ -163,11 +171,13 @@ __device__ __forceinline__ Chunk find_chunk_by_size(const int32_t* __restrict__ 
     k -= hist[g];
   }
   if (g < 1) return ch;
-  int before = 0;  // chunks of g groups of the experts before this pass
+  int before = 0;       // chunks of g groups of the experts before this pass
+  int rows_before = 0;  // padded rows of the experts before this pass
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
     const int m = ChunkSizes<RMAX>::with_groups(n > 0 ? n : 0, g);
     const int incl = wave_inclusive_scan(m);
+    const int pincl = wave_inclusive_scan(padded_rows(n));
     const uint64_t reach = __ballot(before + incl > k);
     if (reach != 0) {
       const int l = __builtin_ctzll(reach);
@@ -179,12 +189,13 @@ __device__ __forceinline__ Chunk find_chunk_by_size(const int32_t* __restrict__ 
       const int idx = g == ChunkSizes<RMAX>::kFull ? i : count - 1;
       const int start = Chunking<RMAX>::kRows * idx;
       ch.expert = base + l;
-      ch.row0 = padded_offsets[base + l] + start;
+      ch.row0 = rows_before + __shfl(pincl - padded_rows(n), l, 64) + start;
       ch.rows = idx + 1 < count ? Chunking<RMAX>::kRows : n_e - start;
       ch.groups = (ch.rows + 31) / 32;
       break;
     }
     before += __shfl(incl, 63, 64);
+    rows_before += __shfl(pincl, 63, 64);
   }
   ch.expert = __builtin_amdgcn_readfirstlane(ch.expert);
   ch.row0 = __builtin_amdgcn_readfirstlane(ch.row0);
@@ -249,14 +260,16 @@ struct LayoutSummary {
   int32_t active;    // experts with at least one row
 };
 
+// first: expert_counts(tokens_per_expert, num_experts, 0), loaded by the
+// caller ahead of its own first dependent load so the two overlap.
 template <int RA, int RB, int RC = 0, int RD = 0>
 __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restrict__ tokens_per_expert,
-                                                          int32_t num_experts) {
+                                                          int32_t num_experts, int32_t first) {
   int64_t rows = 0;
   int32_t most = 0, ca = 0, cb = 0, cc = 0, cd = 0, act = 0;
 #pragma unroll 1
   for (int base = 0; base < num_experts; base += 64) {
-    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
     const int32_t v = n > 0 ? n : 0;
     rows += v;
     most = max(most, v);

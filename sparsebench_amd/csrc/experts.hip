@@ -205,10 +205,12 @@ __global__ void __launch_bounds__(64 * kSddWaves)
   // chunk starts a row block of its own, so there are at most live row
   // blocks x slices tiles either way, numbered up to kNumXcd - 1 chunk rows
   // past them by the XCD deal, plus the split halves of a short last round.
+  // The counts are loaded alongside padded_offsets[E], ahead of the exit test.
+  const int32_t first = expert_counts(tokens_per_expert, num_experts, 0);
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   if (static_cast<int>(blockIdx.x) >= (live_rb + kNumXcd) * (ffn_dim / kSddBN) + tail_slack) return;
   const LayoutSummary sum =
-      summarize_layout<kSddRmax, 4, dsd_rmax<4>(), dsd_rmax<8>()>(tokens_per_expert, num_experts);
+      summarize_layout<kSddRmax, 4, dsd_rmax<4>(), dsd_rmax<8>()>(tokens_per_expert, num_experts, first);
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
   // The DSD's own choice (dsd_layer_kernel): its expert tiles when the
   // routing is balanced and its grid of dsd_grid workgroups holds them all.
@@ -249,14 +251,14 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     if (!balanced_chunk_tile(static_cast<int>(blockIdx.x), chunks, slices, &rank, &slice)) return;
     int32_t hist[kSddRmax + 1];
     chunk_group_hist<kSddRmax>(tokens_per_expert, num_experts, hist);
-    ch = find_chunk_by_size<kSddRmax>(tokens_per_expert, padded_offsets, num_experts, rank, hist);
+    ch = find_chunk_by_size<kSddRmax>(tokens_per_expert, num_experts, rank, hist);
     n0_slice = slice;
   } else {
     const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);
     int c, slice;
     tile_coords(tile, chunks, slices, group, &c, &slice);
     if (c >= chunks) return;
-    ch = find_chunk<kSddRmax>(tokens_per_expert, padded_offsets, num_experts, c);
+    ch = find_chunk<kSddRmax>(tokens_per_expert, num_experts, c);
     n0_slice = slice;
   }
   // Not a routing layout (the chunk would leave the buffers): skip it.
@@ -358,9 +360,10 @@ __global__ void __launch_bounds__(64 * WAVES)
   uint8_t lds[max_int(chunk_lds_bytes<kDsdBN, WAVES, kDsdStages, kRmax>(), max_int(CfgB::kLdsAlloc, CfgH::kLdsAlloc))];
   // As in the SDD: at most live row blocks x D/256 tiles either way, plus
   // the split halves of a short last round.
+  const int32_t first = expert_counts(tokens_per_expert, num_experts, 0);
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   if (static_cast<int>(blockIdx.x) >= live_rb * (d_model / kDsdBN) + tail_slack) return;
-  const LayoutSummary sum = summarize_layout<kRmax, 4>(tokens_per_expert, num_experts);
+  const LayoutSummary sum = summarize_layout<kRmax, 4>(tokens_per_expert, num_experts, first);
   const DsdArgs a{h, w2, out, h_bytes, ffn_dim, d_model};
   // The grid may hold fewer workgroups than expert tiles (see the launch):
   // then the row blocks take the stage.
@@ -390,7 +393,7 @@ __global__ void __launch_bounds__(64 * WAVES)
   int c, slice;
   tile_coords(tile, chunks, slices, group, &c, &slice);
   if (c >= chunks) return;
-  const Chunk ch = find_chunk<kRmax>(tokens_per_expert, padded_offsets, num_experts, c);
+  const Chunk ch = find_chunk<kRmax>(tokens_per_expert, num_experts, c);
   if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kRmax ||
       ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
     return;

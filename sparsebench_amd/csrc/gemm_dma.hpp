@@ -330,6 +330,18 @@ struct DmaMainloop {
 #pragma unroll
     for (int q = 0; q < Dma::kCount; ++q) dma(q);
   }
+  // The first step's loads, B before A: B (the weights) needs no load of its
+  // own to address, while A's offsets may wait on one (the SDD's token rows),
+  // so B's fetch starts under that wait. Step 0's last load is then its A,
+  // and the loads issued after it are those of the later steps, as counted
+  // by every wait below.
+  template <class Dma>
+  __device__ __forceinline__ static void issue_b_first(const Dma& dma) {
+#pragma unroll
+    for (int q = Dma::kA; q < Dma::kCount; ++q) dma(q);
+#pragma unroll
+    for (int q = 0; q < Dma::kA; ++q) dma(q);
+  }
 
   struct NoDma {
     static constexpr int kCount = 0;
@@ -565,9 +577,10 @@ struct DmaMainloop {
     const Frags fr;
     FragA a;
     FragB b;
+    issue_all(b_dma(lds, 0, src));
     issue_all(a_dma(lds, 0, src));
 #pragma unroll
-    for (int u = 0; u < S - 1; ++u)
+    for (int u = 1; u < S - 1; ++u)
       if (u < n) issue_all(b_dma(lds, u, src));
     if (S == 4 && n == 2) wait_vmcnt<kB>();
     else wait_vmcnt<Cfg::kLaterLoadsEven>();
@@ -606,8 +619,9 @@ struct DmaMainloop {
     const Frags fr;
     FragA a;
     FragB b;
+    issue_b_first(step_dma(lds, 0, src));
 #pragma unroll
-    for (int s = 0; s < S - 1; ++s)
+    for (int s = 1; s < S - 1; ++s)
       if (s < n) issue_all(step_dma(lds, s, src));
     wait_steps<Cfg::kLoadsPerStep, S - 2>(n - 1);
     __builtin_amdgcn_s_barrier();
@@ -640,9 +654,10 @@ struct DmaMainloop {
   template <class Src>
   __device__ __forceinline__ static void run_paired(uint8_t* lds, const Src& src, int n, Acc& acc) {
     constexpr int S = Cfg::STAGES;
+    issue_all(b_dma(lds, 0, src));
     issue_all(a_dma(lds, 0, src));
 #pragma unroll
-    for (int u = 0; u < S - 1; ++u)
+    for (int u = 1; u < S - 1; ++u)
       if (u < n) issue_all(b_dma(lds, u, src));
     int t = 0;
     for (; t + S < n; t += 2) {
@@ -687,8 +702,9 @@ struct DmaMainloop {
       run_paired(lds, src, num_steps, acc);
       return;
     }
+    issue_b_first(step_dma(lds, 0, src));
 #pragma unroll
-    for (int s = 0; s < Cfg::STAGES - 1; ++s)
+    for (int s = 1; s < Cfg::STAGES - 1; ++s)
       if (s < num_steps) issue_all(step_dma(lds, s, src));
     if constexpr (Cfg::PIPE == 3 || Cfg::PIPE == 4) {
       // Steps that issue a later step's loads, among their MFMAs; at the top

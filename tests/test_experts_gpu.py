@@ -56,6 +56,9 @@ CASES = {
     "uniform_wide": (lambda s: routing_case("random", 4096, 64, seed=1), 64, 256, 4096),
     # 1024 rows per expert: the SDD keeps row blocks, the DSD takes chunks.
     "few_experts": (lambda s: routing_case("random", 2048, 4, seed=s), 4, 256, 512),
+    # 130 experts of 40-80 rows, every expert one chunk: the SDD's expert
+    # tiles dealt to the XCDs by size, over three passes of 64 experts.
+    "uniform130": (lambda s: routing_case("random", 4000, 130, seed=s), 130, 256, 512),
     # Skewed routing with F % 512 == 0: both layer kernels run row blocks,
     # fewer than one round of them, so each XCD's short round runs as
     # column halves.

@@ -112,8 +112,9 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
  * run when no expert holds more than twice the mean rows, and for SDD also
  * the experts hold at most 256 rows on average: an expert's weights
  * are then streamed once per chunk of up to 192 rows (SDD) or 256 rows
- * (DSD) instead of once per row block, and padding rows past the last
- * 32-row group are neither computed nor read. sb_sdd_experts calls sb_sdd
+ * (DSD; 320 when F >= 8192, a last piece of up to 64 rows joining the
+ * chunk before it) instead of once per row block, and padding rows past
+ * the last 32-row group are neither computed nor read. sb_sdd_experts calls sb_sdd
  * itself when F % 512 != 0, or when max_row_blocks shows more than 256
  * copies per expert (the row blocks would be chosen for all copies valid).
  * The layout arrays are sb_routing's outputs (or those of

@@ -30,6 +30,14 @@ struct Chunking {
   }
 };
 
+__device__ __forceinline__ int wave_inclusive_scan(int v);
+// Sum of v over the wave (every lane gets it).
+__device__ __forceinline__ int wave_inclusive_scan_total(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -121,49 +129,32 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
   return ch;
 }
 
-// Chunks by row-group count. An expert with n rows has c = count(n) chunks:
-// c - 1 full ones of kRows / 32 groups and a last one of
-// ceil((n - kRows (c - 1)) / 32) groups (up to RMAX with a joined piece).
+// The experts by tile size, for layouts where every expert is one chunk:
+// hist[g] = experts of g row groups (ceil(n / 32) = g), g = 1 .. RMAX, from
+// one ballot per g and pass (every wave computes the same values).
 template <int RMAX>
-struct ChunkSizes {
-  static constexpr int kFull = Chunking<RMAX>::kRows / 32;
-  // Chunks of this expert with exactly g groups.
-  __device__ __forceinline__ static int with_groups(int32_t n, int g) {
-    const int c = Chunking<RMAX>::count(n);
-    if (c == 0) return 0;
-    const int last = (n - Chunking<RMAX>::kRows * (c - 1) + 31) / 32;
-    return (g == kFull ? c - 1 : 0) + (g == last ? 1 : 0);
-  }
-};
-
-// hist[g] = chunks of g row groups over all experts, g = 1 .. RMAX (every
-// wave computes the same values).
-template <int RMAX>
-__device__ __forceinline__ void chunk_group_hist(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
-                                                 int32_t (&hist)[RMAX + 1]) {
-  int32_t h[RMAX + 1] = {};
+__device__ __forceinline__ void single_chunk_hist(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
+                                                  int32_t (&hist)[RMAX + 1]) {
+#pragma unroll
+  for (int g = 0; g <= RMAX; ++g) hist[g] = 0;
 #pragma unroll 1
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int groups = n > 0 ? (n + 31) / 32 : 0;
 #pragma unroll
-    for (int g = 1; g <= RMAX; ++g) h[g] += ChunkSizes<RMAX>::with_groups(n > 0 ? n : 0, g);
+    for (int g = 1; g <= RMAX; ++g) hist[g] += __builtin_popcountll(__ballot(groups == g));
   }
-#pragma unroll
-  for (int g = 1; g <= RMAX; ++g) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) h[g] += __shfl_xor(h[g], d, 64);
-    hist[g] = __builtin_amdgcn_readfirstlane(h[g]);
-  }
-  hist[0] = 0;
 }
 
-// Chunk k (0 <= k < the number of chunks) in size order: by row-group count,
-// largest first, and in expert order within one count (an expert's full
-// chunks before its last one), so the k-th chunk of that order and the
-// chunks of find_chunk are the same set.
+// Chunk k (0 <= k < the number of experts with rows) in size order, for
+// layouts where every expert is one chunk: by row-group count, largest
+// first, in expert order within one count. The chunk's first row is the sum
+// of the padded rows of the experts before it (padded_offsets[e] of the
+// routing layout), computed from the counts.
 template <int RMAX>
-__device__ __forceinline__ Chunk find_chunk_by_size(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
-                                                    int k, const int32_t (&hist)[RMAX + 1]) {
+__device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __restrict__ tokens_per_expert,
+                                                           int32_t num_experts, int k,
+                                                           const int32_t (&hist)[RMAX + 1]) {
   Chunk ch{-1, 0, 0, 0};
   int g = RMAX;
   for (; g >= 1; --g) {  // the count that holds rank k, and k's rank within it
@@ -171,31 +162,26 @@ __device__ __forceinline__ Chunk find_chunk_by_size(const int32_t* __restrict__ 
     k -= hist[g];
   }
   if (g < 1) return ch;
-  int before = 0;       // chunks of g groups of the experts before this pass
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int rows_before = 0;  // padded rows of the experts before this pass
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
-    const int m = ChunkSizes<RMAX>::with_groups(n > 0 ? n : 0, g);
-    const int incl = wave_inclusive_scan(m);
-    const int pincl = wave_inclusive_scan(padded_rows(n));
-    const uint64_t reach = __ballot(before + incl > k);
-    if (reach != 0) {
-      const int l = __builtin_ctzll(reach);
-      const int i = k - (before + __shfl(incl - m, l, 64));
-      const int32_t n_e = __shfl(n, l, 64);
-      const int count = Chunking<RMAX>::count(n_e);
-      // The expert's chunks of g groups are its first m (all full ones, g
-      // = kFull) or its last one.
-      const int idx = g == ChunkSizes<RMAX>::kFull ? i : count - 1;
-      const int start = Chunking<RMAX>::kRows * idx;
+    const uint64_t match = __ballot(n > 0 && (n + 31) / 32 == g);
+    const int cnt = __builtin_popcountll(match);
+    if (k < cnt) {
+      // The lane of the k-th match: its rank among the matches is k.
+      const uint64_t hit = __ballot(((match >> lane) & 1) && __builtin_popcountll(match & below) == k);
+      const int l = __builtin_ctzll(hit);
+      const int pincl = wave_inclusive_scan(padded_rows(n));
       ch.expert = base + l;
-      ch.row0 = rows_before + __shfl(pincl - padded_rows(n), l, 64) + start;
-      ch.rows = idx + 1 < count ? Chunking<RMAX>::kRows : n_e - start;
-      ch.groups = (ch.rows + 31) / 32;
+      ch.row0 = rows_before + __shfl(pincl - padded_rows(n), l, 64);
+      ch.rows = __shfl(n, l, 64);
+      ch.groups = g;
       break;
     }
-    before += __shfl(incl, 63, 64);
-    rows_before += __shfl(pincl, 63, 64);
+    k -= cnt;
+    rows_before += wave_inclusive_scan_total(padded_rows(n));
   }
   ch.expert = __builtin_amdgcn_readfirstlane(ch.expert);
   ch.row0 = __builtin_amdgcn_readfirstlane(ch.row0);

@@ -250,8 +250,8 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     int rank, slice;
     if (!balanced_chunk_tile(static_cast<int>(blockIdx.x), chunks, slices, &rank, &slice)) return;
     int32_t hist[kSddRmax + 1];
-    chunk_group_hist<kSddRmax>(tokens_per_expert, num_experts, hist);
-    ch = find_chunk_by_size<kSddRmax>(tokens_per_expert, num_experts, rank, hist);
+    single_chunk_hist<kSddRmax>(tokens_per_expert, num_experts, hist);
+    ch = find_single_chunk_by_size<kSddRmax>(tokens_per_expert, num_experts, rank, hist);
     n0_slice = slice;
   } else {
     const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);

@@ -129,6 +129,53 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
   return ch;
 }
 
+// Largest-first order inside one tile group (the `group` chunks g0 .. g0+G-1
+// that tile_coords walks slice by slice): the chunks with more than
+// kRows / 32 row groups (an expert's last chunk with a joined piece) take
+// the group's first tiles, all their slices, then the others slice by
+// slice. Chunk p of the group is such a chunk iff bit p of the returned
+// mask is set. One pass over the counts.
+template <int RMAX>
+__device__ __forceinline__ uint32_t big_chunks_of_group(const int32_t* __restrict__ tokens_per_expert,
+                                                        int32_t num_experts, int g0, int G) {
+  constexpr int kFull = Chunking<RMAX>::kRows / 32;
+  uint32_t mask = 0;
+  int before = 0;
+  for (int base = 0; base < num_experts && before < g0 + G; base += 64) {
+    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int c = Chunking<RMAX>::count(n);
+    const int incl = wave_inclusive_scan(c);
+    const int last = before + incl - 1;  // this expert's last chunk
+    const int groups = c > 0 ? (n - Chunking<RMAX>::kRows * (c - 1) + 31) / 32 : 0;
+    uint32_t bit = (c > 0 && groups > kFull && last >= g0 && last < g0 + G) ? (1u << (last - g0)) : 0u;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) bit |= __shfl_xor(bit, d, 64);
+    mask |= bit;
+    before += __shfl(incl, 63, 64);
+  }
+  return __builtin_amdgcn_readfirstlane(mask);
+}
+
+// Local tile `local` of a group of G chunks x `slices` slices, largest
+// first: the chunks of `big` (a mask over the group's positions) with all
+// their slices, then the rest slice by slice.
+__device__ __forceinline__ void lpt_group_tile(int local, int G, int slices, uint32_t big, int* pos, int* slice) {
+  const int nb = __builtin_popcount(big);
+  uint32_t set = big;
+  int idx;
+  if (local < nb * slices) {
+    idx = local % nb;
+    *slice = local / nb;
+  } else {
+    local -= nb * slices;
+    set = ~big & ((G >= 32 ? 0u : (1u << G)) - 1u);
+    idx = local % (G - nb);
+    *slice = local / (G - nb);
+  }
+  for (int i = 0; i < idx; ++i) set &= set - 1;  // drop the idx lowest members
+  *pos = __builtin_ctz(set);
+}
+
 // The experts by tile size, for layouts where every expert is one chunk:
 // hist[g] = experts of g row groups (ceil(n / 32) = g), g = 1 .. RMAX, from
 // one ballot per g and pass (every wave computes the same values).
@@ -218,10 +265,14 @@ __device__ __forceinline__ bool balanced_chunk_tile(int bid, int chunks, int sli
 //             blocks: their tiles are all one size, and the many row blocks
 //             of a popular expert run side by side and share its W2 lines
 //             in L2, where chunks of very different sizes leave CUs idle.
-//   kGateSdd  as kGateDsd, and at most 256 rows per expert on average: the
-//             case where merging an expert's last, nearly empty row block
-//             into one tile saves a whole stream of its W1 slice (with many
-//             blocks per expert the row-block tiles are faster). The SDD's
+//   kGateSdd  as kGateDsd, and either at most 256 rows per expert on
+//             average (merging an expert's last, nearly empty row block
+//             into one tile saves a whole stream of its W1 slice), or
+//             fewer rounds of tiles over the CUs than the row blocks need
+//             (large experts: each expert's last, nearly empty row block is
+//             a tile of its own among the row blocks, which can add a
+//             round; with as many rounds the row-block tiles are as fast
+//             and need no summary of the layout). The SDD's
 //             expert tiles leave padding rows past each expert's last
 //             32-row group unwritten, so they must only feed the DSD's
 //             expert tiles, which do not read them: the SDD takes its
@@ -286,9 +337,17 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
   return sum;
 }
 
-__device__ __forceinline__ bool expert_tiles_chosen(const LayoutSummary& sum, int32_t num_experts, int32_t gate) {
+__device__ __forceinline__ bool expert_tiles_chosen(const LayoutSummary& sum, int32_t num_experts, int32_t gate,
+                                                    int32_t slices, int32_t cus) {
   const bool balanced = sum.rows > 0 && static_cast<int64_t>(sum.largest) * num_experts <= 2 * sum.rows;
-  const bool chosen = gate == kGateSdd ? balanced && sum.rows <= static_cast<int64_t>(256) * num_experts : balanced;
+  bool chosen = balanced;
+  if (gate == kGateSdd) {
+    // Rounds of 512-wide tiles over the CUs: large experts take the expert
+    // chunks when these need fewer rounds than the row blocks.
+    const int64_t chunk_rounds = (static_cast<int64_t>(sum.chunks_a) * slices + cus - 1) / cus;
+    const int64_t block_rounds = (static_cast<int64_t>(sum.chunks_b) * slices + cus - 1) / cus;
+    chosen = balanced && (sum.rows <= static_cast<int64_t>(256) * num_experts || chunk_rounds < block_rounds);
+  }
   return __builtin_amdgcn_readfirstlane(chosen ? 1 : 0) != 0;
 }
 
@@ -302,10 +361,10 @@ inline int32_t expert_gate_override() {
 // On the device: are the expert tiles of `gate`'s stage used?
 // force: 0 choose, 1 always, 2 never.
 __device__ __forceinline__ bool expert_stage_runs(const LayoutSummary& sum, int32_t num_experts, int32_t gate,
-                                                  int32_t force) {
+                                                  int32_t force, int32_t slices = 1, int32_t cus = 1) {
   if (force == 1) return true;
   if (force == 2) return false;
-  return expert_tiles_chosen(sum, num_experts, gate);
+  return expert_tiles_chosen(sum, num_experts, gate, slices, cus);
 }
 
 }  // namespace sb

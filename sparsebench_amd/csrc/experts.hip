@@ -218,7 +218,8 @@ __global__ void __launch_bounds__(64 * kSddWaves)
                                          static_cast<int64_t>(ffn_dim >= kDsdDeepF ? sum.chunks_d : sum.chunks_c) *
                                                  (d_model / kDsdBN) <=
                                              dsd_grid);
-  if (!(expert_stage_runs(sum, num_experts, kGateSdd, force) && dsd_expert)) {
+  if (!(expert_stage_runs(sum, num_experts, kGateSdd, force, ffn_dim / kSddBN, cus_per_xcd * kNumXcd) &&
+        dsd_expert)) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in
     // order; every row is computed and written (padding rows read as zeros).
     // The tiles of a short last round run as column halves (split_tail).
@@ -254,12 +255,18 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     ch = find_single_chunk_by_size<kSddRmax>(tokens_per_expert, num_experts, rank, hist);
     n0_slice = slice;
   } else {
+    // Groups of `group` chunks x slices (tile_coords), largest chunks first
+    // inside each group (lpt_group_tile).
     const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);
-    int c, slice;
-    tile_coords(tile, chunks, slices, group, &c, &slice);
-    if (c >= chunks) return;
-    ch = find_chunk<kSddRmax>(tokens_per_expert, num_experts, c);
-    n0_slice = slice;
+    if (tile >= chunks * slices) return;
+    const int per_group = group * slices;
+    const int g0 = (tile / per_group) * group;
+    const int G = min(group, chunks - g0);
+    const uint32_t big = big_chunks_of_group<kSddRmax>(tokens_per_expert, num_experts, g0, G);
+    int pos, slice;
+    lpt_group_tile(tile - (g0 / group) * per_group, G, slices, big, &pos, &slice);
+    ch = find_chunk<kSddRmax>(tokens_per_expert, num_experts, __builtin_amdgcn_readfirstlane(g0 + pos));
+    n0_slice = __builtin_amdgcn_readfirstlane(slice);
   }
   // Not a routing layout (the chunk would leave the buffers): skip it.
   if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kSddRmax ||
@@ -538,18 +545,12 @@ extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_
     return fail(SB_ERR_INVALID, "problem too large");
   const int32_t force = expert_gate_override();
   // The expert tiles are 512 wide; other widths take the per-row-block kernel.
-  // So do layouts of more than 256 copies per expert on average: the worst-
-  // case row block count, floor((n + 127 E) / 128), bounds the copies n from
-  // below, and with n rows the device would choose the row blocks too. It
-  // could choose otherwise only if many copies were dropped (bad expert ids,
-  // tokens past valid_tokens); the real rows are the same bits either way,
-  // and the per-row-block kernel skips the summary every layer workgroup
-  // computes first. The layer kernel reads x and W1[e] through 32-bit buffer
-  // offsets; x of 2 GiB or more, or one expert's W1 of 2 GiB or more, also
-  // go to the per-row-block kernel, which gathers x with 64-bit addresses.
-  const int64_t min_copies = max_row_blocks * kBS - num_experts * (kBS - 1);
+  // The layer kernel reads x and W1[e] through 32-bit buffer offsets; x of
+  // 2 GiB or more, or one expert's W1 of 2 GiB or more, also go to the
+  // per-row-block kernel, which gathers x with 64-bit addresses. The real
+  // rows are the same bits either way.
   const bool offsets_fit = !sdd_wide_x(num_tokens, d_model) && ffn_dim * d_model * 2 < (int64_t{1} << 31);
-  if (ffn_dim % kSddBN != 0 || force == 2 || !offsets_fit || (force != 1 && min_copies > 256 * num_experts))
+  if (ffn_dim % kSddBN != 0 || force == 2 || !offsets_fit)
     return sb_sdd(x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
                   max_row_blocks, apply_gelu, stream);
   const int rc = dispatch_sdd_layer(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert, padded_offsets,

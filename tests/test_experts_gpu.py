@@ -54,7 +54,8 @@ CASES = {
     # The fine-grained shape's routing (every expert <= 160 rows with this
     # seed) and F: 64 x 8 expert SDD tiles, 2 rounds on 256 CUs.
     "uniform_wide": (lambda s: routing_case("random", 4096, 64, seed=1), 64, 256, 4096),
-    # 1024 rows per expert: the SDD keeps row blocks, the DSD takes chunks.
+    # 1024 rows per expert: a handful of tiles either way (one round), so
+    # the SDD keeps row blocks; the DSD takes chunks.
     "few_experts": (lambda s: routing_case("random", 2048, 4, seed=s), 4, 256, 512),
     # 130 experts of 40-80 rows, every expert one chunk: the SDD's expert
     # tiles dealt to the XCDs by size, over three passes of 64 experts.
@@ -65,7 +66,9 @@ CASES = {
     "zipf_rows": (lambda s: routing_case("zipf_perm", 2000, 32, seed=s), 32, 512, 1024),
     # The Mixtral-like shape's routing (971-1057 rows per expert with seed 0)
     # with F >= 8192: the DSD's 8-wave expert tiles join a last piece of up
-    # to 64 rows to the chunk before it (tiles of 9 and 10 row groups).
+    # to 64 rows to the chunk before it (tiles of 9 and 10 row groups); the
+    # SDD's 64 chunks x 16 slices fill 4 rounds on 256 CUs against 5 for the
+    # 69 row blocks, so it takes its chunks too (largest first in each group).
     "big_experts": (lambda s: routing_case("random", 4096, 8, seed=0), 8, 256, 8192),
     # A reduction of F >= 8192: the DSD's 8-wave tiles (row blocks, and
     # chunks of every row-group count: odd ones in one row of 8 waves, even
@@ -291,16 +294,23 @@ def dsd_chunks(counts: list[int], f: int) -> int:
     return sum(chunk_count(c, 256, merge) for c in counts)
 
 
-def gate_rule(counts: list[int], stage: str, max_rb: int, d: int, f: int) -> bool:
+def gate_rule(counts: list[int], stage: str, max_rb: int, d: int, f: int, cus: int = 256) -> bool:
     """The choice stated in expert_chunks.hpp, restated: the DSD takes expert
     tiles iff no expert holds more than twice the mean rows and its grid
-    holds all of them; the SDD iff, besides, the mean is at most 256 rows
-    and the DSD takes its expert tiles."""
+    holds all of them; the SDD iff the DSD does and, besides, the mean is at
+    most 256 rows or its expert chunks (128 rows, a last piece of up to 64
+    joined) fill fewer rounds of 512-wide tiles over the CUs than the row
+    blocks."""
     counts = [max(c, 0) for c in counts]
     total, most, e = sum(counts), max(counts), len(counts)
     balanced = total > 0 and most * e <= 2 * total
     dsd = balanced and dsd_chunks(counts, f) * (d // 256) <= dsd_grid(max_rb, e, d)
-    return dsd and (stage == "dsd" or total <= 256 * e)
+    if stage == "dsd" or not dsd:
+        return dsd
+    slices = f // 512
+    chunk_rounds = -(-sum(chunk_count(c, 128, 64) for c in counts) * slices // cus)
+    block_rounds = -(-sum(-(-c // 128) for c in counts) * slices // cus)
+    return total <= 256 * e or chunk_rounds < block_rounds
 
 
 @pytest.mark.parametrize("case", list(CASES))
@@ -317,6 +327,7 @@ def test_device_choice_follows_the_rule(case: str) -> None:
     topo = route_device(idx.cuda(), e, f, 128)
     counts = topo.tokens_per_expert.cpu().tolist()
     max_rb = topo.row_token.numel() // 128
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
     fb = f // 128
     xc, w1c, w2c = x.cuda(), w1.cuda(), w2.cuda().view(e * f, d)
     h = torch.full((max_rb * fb, 128, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
@@ -339,10 +350,10 @@ def test_device_choice_follows_the_rule(case: str) -> None:
     dense = dense_rows(h, fb)
     if f % 512 == 0 and untouched:
         sdd_expert = bool(torch.isnan(dense[torch.tensor(untouched, device="cuda")]).all())
-        assert sdd_expert == gate_rule(counts, "sdd", max_rb, d, f)
+        assert sdd_expert == gate_rule(counts, "sdd", max_rb, d, f, cus)
     if pad:
         dsd_expert = bool(torch.isnan(y[torch.tensor(pad, device="cuda")]).all())
-        assert dsd_expert == gate_rule(counts, "dsd", max_rb, d, f)
+        assert dsd_expert == gate_rule(counts, "dsd", max_rb, d, f, cus)
 
 
 def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(monkeypatch) -> None:

@@ -108,15 +108,17 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
  * spmm.sdd then spmm.dsd version 5 on route_device's layout). Each call
  * enqueues one kernel whose workgroups choose, on the GPU and all alike from
  * tokens_per_expert, between tiles that follow each expert's real rows and
- * row-block tiles of sb_sdd's / sb_dsd's default shape. The expert tiles
- * run when no expert holds more than twice the mean rows, and for SDD also
- * the experts hold at most 256 rows on average: an expert's weights
+ * row-block tiles of sb_sdd's / sb_dsd's default shape. The DSD's expert
+ * tiles run when no expert holds more than twice the mean rows and the
+ * DSD's grid holds them; the SDD's run when the DSD's do and either the
+ * experts hold at most 256 rows on average or the expert tiles need fewer
+ * rounds over the device's CUs than the row blocks. An expert's weights
  * are then streamed once per chunk of up to 192 rows (SDD) or 256 rows
  * (DSD; 320 when F >= 8192, a last piece of up to 64 rows joining the
  * chunk before it) instead of once per row block, and padding rows past
  * the last 32-row group are neither computed nor read. sb_sdd_experts calls sb_sdd
- * itself when F % 512 != 0, or when max_row_blocks shows more than 256
- * copies per expert (the row blocks would be chosen for all copies valid).
+ * itself when F % 512 != 0, or when x or one expert's W1 is 2 GiB or more
+ * (the layer kernel addresses them with 32-bit offsets).
  * The layout arrays are sb_routing's outputs (or those of
  * sb_routing_assigned / sb_token_rounding); max_row_blocks is its
  * worst-case row block count and num_copies the length of its copy_row.

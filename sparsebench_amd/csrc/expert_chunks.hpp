@@ -30,23 +30,43 @@ struct Chunking {
   }
 };
 
-__device__ __forceinline__ int wave_inclusive_scan(int v);
-// Sum of v over the wave (every lane gets it).
-__device__ __forceinline__ int wave_inclusive_scan_total(int v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+// Inclusive prefix sum of v over the wave's 64 lanes (lane i gets lanes
+// 0 .. i) by DPP moves, six VALU operations: row_shr 1, 2, 4 and 8 add up
+// each row of 16 lanes, then row_bcast:15 adds row 0's total to row 1 and
+// row 2's to row 3, and row_bcast:31 adds the total of rows 0-1 to rows 2
+// and 3. A lane whose source lies outside its row, or whose row the row
+// mask leaves out, adds the 0 it starts from. Every lane of the wave must
+// be active. (A shuffle through LDS, ds_bpermute, is a round trip of its
+// own: six dependent ones per scan made the layout summary and the chunk
+// search a few microseconds of every tile's start.)
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return v;
 }
 
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int u = __shfl_up(v, d, 64);
-    if (lane >= d) v += u;
-  }
+// The same scan with max, for v >= 0.
+__device__ __forceinline__ int wave_inclusive_max(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));
   return v;
 }
+
+// Sum of v over the wave, as a uniform (scalar) value.
+__device__ __forceinline__ int wave_inclusive_scan_total(int v) {
+  return __builtin_amdgcn_readlane(wave_inclusive_scan(v), 63);
+}
+
+// Lane l's v, for a uniform l: a scalar read (v_readlane_b32).
+__device__ __forceinline__ int lane_value(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 
 // tokens_per_expert[base + lane] (0 past the experts) for one pass of 64
 // experts. The addresses are uniform, so these are scalar loads: after a
@@ -109,18 +129,18 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
     const uint64_t reach = __ballot(before + incl > c);  // experts whose chunks run past c
     if (reach != 0) {
       const int l = __builtin_ctzll(reach);  // the first of them holds chunk c
-      const int i = c - (before + __shfl(incl - cc, l, 64));
-      const int count = __shfl(cc, l, 64);
-      const int32_t n_e = __shfl(n, l, 64);
+      const int i = c - (before + lane_value(incl - cc, l));
+      const int count = lane_value(cc, l);
+      const int32_t n_e = lane_value(n, l);
       const int start = Chunking<RMAX>::kRows * i;
       ch.expert = base + l;
-      ch.row0 = rows_before + __shfl(pincl - padded_rows(n), l, 64) + start;
+      ch.row0 = rows_before + lane_value(pincl - padded_rows(n), l) + start;
       ch.rows = i + 1 < count ? Chunking<RMAX>::kRows : n_e - start;
       ch.groups = (ch.rows + 31) / 32;
       break;
     }
-    before += __shfl(incl, 63, 64);
-    rows_before += __shfl(pincl, 63, 64);
+    before += lane_value(incl, 63);
+    rows_before += lane_value(pincl, 63);
   }
   ch.expert = __builtin_amdgcn_readfirstlane(ch.expert);
   ch.row0 = __builtin_amdgcn_readfirstlane(ch.row0);
@@ -147,11 +167,11 @@ __device__ __forceinline__ uint32_t big_chunks_of_group(const int32_t* __restric
     const int incl = wave_inclusive_scan(c);
     const int last = before + incl - 1;  // this expert's last chunk
     const int groups = c > 0 ? (n - Chunking<RMAX>::kRows * (c - 1) + 31) / 32 : 0;
-    uint32_t bit = (c > 0 && groups > kFull && last >= g0 && last < g0 + G) ? (1u << (last - g0)) : 0u;
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) bit |= __shfl_xor(bit, d, 64);
-    mask |= bit;
-    before += __shfl(incl, 63, 64);
+    const uint32_t bit = (c > 0 && groups > kFull && last >= g0 && last < g0 + G) ? (1u << (last - g0)) : 0u;
+    // Experts have distinct last chunks, so their bits are distinct and
+    // the wave's sum is their union.
+    mask |= static_cast<uint32_t>(wave_inclusive_scan_total(static_cast<int>(bit)));
+    before += lane_value(incl, 63);
   }
   return __builtin_amdgcn_readfirstlane(mask);
 }
@@ -209,8 +229,6 @@ __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __rest
     k -= hist[g];
   }
   if (g < 1) return ch;
-  const int lane = threadIdx.x & 63;
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int rows_before = 0;  // padded rows of the experts before this pass
   for (int base = 0; base < num_experts; base += 64) {
     const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
@@ -218,12 +236,14 @@ __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __rest
     const int cnt = __builtin_popcountll(match);
     if (k < cnt) {
       // The lane of the k-th match: its rank among the matches is k.
-      const uint64_t hit = __ballot(((match >> lane) & 1) && __builtin_popcountll(match & below) == k);
+      const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(match >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(match), 0));
+      const uint64_t hit = __ballot(n > 0 && (n + 31) / 32 == g && below == k);
       const int l = __builtin_ctzll(hit);
       const int pincl = wave_inclusive_scan(padded_rows(n));
       ch.expert = base + l;
-      ch.row0 = rows_before + __shfl(pincl - padded_rows(n), l, 64);
-      ch.rows = __shfl(n, l, 64);
+      ch.row0 = rows_before + lane_value(pincl - padded_rows(n), l);
+      ch.rows = lane_value(n, l);
       ch.groups = g;
       break;
     }
@@ -316,24 +336,18 @@ __device__ __forceinline__ LayoutSummary summarize_layout(const int32_t* __restr
     if constexpr (RC > 0) cc += Chunking<RC>::count(v);
     if constexpr (RD > 0) cd += Chunking<RD>::count(v);
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    rows += __shfl_xor(rows, d, 64);
-    most = max(most, __shfl_xor(most, d, 64));
-    ca += __shfl_xor(ca, d, 64);
-    cb += __shfl_xor(cb, d, 64);
-    if constexpr (RC > 0) cc += __shfl_xor(cc, d, 64);
-    if constexpr (RD > 0) cd += __shfl_xor(cd, d, 64);
-    act += __shfl_xor(act, d, 64);
-  }
+  // A lane's row sum (under 2^35) is split at bit 16 so that each half's
+  // sum over the wave stays under 2^31.
   LayoutSummary sum;
-  sum.rows = rows;
-  sum.largest = __builtin_amdgcn_readfirstlane(most);
-  sum.chunks_a = __builtin_amdgcn_readfirstlane(ca);
-  sum.chunks_b = __builtin_amdgcn_readfirstlane(cb);
-  sum.chunks_c = __builtin_amdgcn_readfirstlane(cc);
-  sum.chunks_d = __builtin_amdgcn_readfirstlane(cd);
-  sum.active = __builtin_amdgcn_readfirstlane(act);
+  const int64_t lo = wave_inclusive_scan_total(static_cast<int>(rows & 0xffff));
+  const int64_t hi = wave_inclusive_scan_total(static_cast<int>(rows >> 16));
+  sum.rows = (hi << 16) + lo;
+  sum.largest = __builtin_amdgcn_readlane(wave_inclusive_max(most), 63);
+  sum.chunks_a = wave_inclusive_scan_total(ca);
+  sum.chunks_b = wave_inclusive_scan_total(cb);
+  sum.chunks_c = RC > 0 ? wave_inclusive_scan_total(cc) : 0;
+  sum.chunks_d = RD > 0 ? wave_inclusive_scan_total(cd) : 0;
+  sum.active = wave_inclusive_scan_total(act);
   return sum;
 }
 

@@ -116,9 +116,11 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
  * are then streamed once per chunk of up to 192 rows (SDD) or 256 rows
  * (DSD; 320 when F >= 8192, a last piece of up to 64 rows joining the
  * chunk before it) instead of once per row block, and padding rows past
- * the last 32-row group are neither computed nor read. sb_sdd_experts calls sb_sdd
- * itself when F % 512 != 0, or when x or one expert's W1 is 2 GiB or more
- * (the layer kernel addresses them with 32-bit offsets).
+ * the last 32-row group are neither computed nor read. For F % 512 != 0
+ * sb_sdd_experts tiles each expert's row blocks in pairs (256 x 256 tiles,
+ * an odd last one alone) and writes every padded row, as sb_sdd does. It
+ * calls sb_sdd itself when x or one expert's W1 is 2 GiB or more (the layer
+ * kernels address them with 32-bit offsets).
  * The layout arrays are sb_routing's outputs (or those of
  * sb_routing_assigned / sb_token_rounding); max_row_blocks is its
  * worst-case row block count and num_copies the length of its copy_row.

@@ -253,7 +253,8 @@ def _check_expert_layout(topo, device: torch.device) -> None:
 
 def sdd_experts_cuda(x: torch.Tensor, w1: torch.Tensor, topo, apply_gelu: bool) -> torch.Tensor:
     """SDD of the MoE layer (this build's addition): expert-major tiles when
-    the routing is balanced, else the per-row-block kernel, chosen on the GPU.
+    the routing is balanced, else row-block tiles, chosen on the GPU; for
+    F % 512 != 0, each expert's row blocks in pairs (every row written).
 
     topo: a routing layout from route_device / route_assigned / route_rounded.
     Returns H blocks [max_row_blocks*F/128, 128, 128] bf16 whose real rows are

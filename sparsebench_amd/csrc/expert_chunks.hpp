@@ -257,6 +257,111 @@ __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __rest
   return ch;
 }
 
+// Row-block pairs, the SDD's units when F % 512 != 0 (256-wide tiles): an
+// expert's row blocks two by two from its first, an odd last one alone. A
+// pair is 256 padded rows (8 row groups), a single 128 (4); the tile
+// computes every padded row, so padding rows come out as zeros, as from the
+// per-row-block kernel. Units are numbered in expert order, each expert's
+// pairs before its single. For spreading them over the XCDs a pair costs
+// kPairCost and a single kSingleCost: measured tile times at D = 2048
+// (config 5), 69 and 48 us.
+constexpr int kPairCost = 10, kSingleCost = 7;
+
+struct PairCounts {
+  int32_t pairs, singles, cost;
+};
+
+// first: expert_counts(tokens_per_expert, num_experts, 0).
+__device__ __forceinline__ PairCounts pair_counts(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
+                                                  int32_t first) {
+  int p = 0, s = 0;
+#pragma unroll 1
+  for (int base = 0; base < num_experts; base += 64) {
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
+    const int rb = n > 0 ? (n + kBS - 1) / kBS : 0;
+    p += rb >> 1;
+    s += rb & 1;
+  }
+  PairCounts c;
+  c.pairs = wave_inclusive_scan_total(p);
+  c.singles = wave_inclusive_scan_total(s);
+  c.cost = c.pairs * kPairCost + c.singles * kSingleCost;
+  return c;
+}
+
+// The first unit whose cost start (the summed cost of the units before it)
+// is at least `target`, as the numbers of pairs and of singles before it
+// (all of them if there is none).
+struct UnitsBefore {
+  int32_t pairs, singles;
+};
+
+__device__ __forceinline__ UnitsBefore first_pair_unit_at(const int32_t* __restrict__ tokens_per_expert,
+                                                          int32_t num_experts, int target, int32_t first) {
+  int cost_before = 0, pairs_before = 0, singles_before = 0;  // over the experts before this pass
+#pragma unroll 1
+  for (int base = 0; base < num_experts; base += 64) {
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
+    const int rb = n > 0 ? (n + kBS - 1) / kBS : 0;
+    const int p = rb >> 1, sg = rb & 1;
+    const int cost = p * kPairCost + sg * kSingleCost;
+    const int cincl = wave_inclusive_scan(cost);
+    const int pincl = wave_inclusive_scan(p);
+    const int sincl = wave_inclusive_scan(sg);
+    if (target < cost_before + lane_value(cincl, 63)) {
+      const int l = __builtin_ctzll(__ballot(cost_before + cincl > target));  // the expert whose costs cover target
+      const int off = target - (cost_before + lane_value(cincl - cost, l));   // 0 <= off < its cost
+      const int p_l = lane_value(p, l);
+      // Its units start at off 0, kPairCost, ..., p_l * kPairCost (the single).
+      const int i = off <= 0 ? 0 : (off <= p_l * kPairCost ? (off + kPairCost - 1) / kPairCost : p_l + 1);
+      UnitsBefore u;
+      u.pairs = pairs_before + lane_value(pincl - p, l) + min(i, p_l);
+      u.singles = singles_before + lane_value(sincl - sg, l) + (i > p_l ? 1 : 0);
+      return u;
+    }
+    cost_before += lane_value(cincl, 63);
+    pairs_before += lane_value(pincl, 63);
+    singles_before += lane_value(sincl, 63);
+  }
+  return {pairs_before, singles_before};
+}
+
+// Pair k (single = false) or single k (single = true), each kind counted in
+// expert order. The chunk's first row is the sum of the padded rows of the
+// experts before it (padded_offsets[e] of the routing layout), computed
+// from the counts.
+__device__ __forceinline__ Chunk find_pair_unit(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
+                                                bool single, int k, int32_t first) {
+  Chunk ch{-1, 0, 0, 0};
+  int rows_before = 0;  // padded rows of the experts before this pass
+#pragma unroll 1
+  for (int base = 0; base < num_experts; base += 64) {
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
+    const int rb = n > 0 ? (n + kBS - 1) / kBS : 0;
+    const int mine = single ? (rb & 1) : (rb >> 1);  // this expert's units of the kind
+    const int incl = wave_inclusive_scan(mine);
+    const int total = lane_value(incl, 63);
+    if (k < total) {
+      const int l = __builtin_ctzll(__ballot(incl > k));  // the expert that holds unit k
+      const int i = k - (lane_value(incl, l) - lane_value(mine, l));
+      const int first_rb = single ? lane_value(rb, l) - 1 : 2 * i;  // the unit's first row block in the expert
+      const int pincl = wave_inclusive_scan(rb * kBS);
+      ch.expert = base + l;
+      ch.row0 = rows_before + lane_value(pincl - rb * kBS, l) + first_rb * kBS;
+      ch.rows = min(lane_value(n, l) - first_rb * kBS, single ? kBS : 2 * kBS);
+      ch.groups = single ? 4 : 8;
+      break;
+    }
+    k -= total;
+    rows_before += wave_inclusive_scan_total(rb * kBS);
+  }
+  ch.expert = __builtin_amdgcn_readfirstlane(ch.expert);
+  ch.row0 = __builtin_amdgcn_readfirstlane(ch.row0);
+  ch.rows = __builtin_amdgcn_readfirstlane(ch.rows);
+  ch.groups = __builtin_amdgcn_readfirstlane(ch.groups);
+  return ch;
+}
+
 // The XCD-balanced tile of workgroup bid over `chunks` chunks x `slices`
 // column slices. The chunks in size order are dealt to the XCDs like cards
 // in snake order (ranks 0-7 to XCDs 0-7, ranks 8-15 to XCDs 7-0, ...), so

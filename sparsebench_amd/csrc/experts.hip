@@ -278,6 +278,66 @@ __global__ void __launch_bounds__(64 * kSddWaves)
   });
 }
 
+// The SDD for F % 512 != 0: 256-wide tiles over row-block pairs
+// (expert_chunks.hpp). A pair is one 256 x 256 tile of 8 waves (two rows of
+// 4, 128 x 64 each), so each W1 slice is streamed once per two row blocks
+// of an expert instead of once per row block; a single is the per-row-block
+// kernel's 128 x 256 tile. XCD x takes the units whose cost starts fall in
+// the x-th eighth of the total, so the XCDs get like shares of the work and
+// an expert's units stay on one or two XCDs, which then stream its W1 from
+// HBM once. An XCD runs its pairs, then its singles, so the tiles handed to
+// the CUs that free up last are the short ones; a unit's slices run side by
+// side (sharing its x rows), and so do an expert's pairs (sharing its W1
+// slices). Every padded row is written, so either DSD tiling may follow.
+using SddPairTile = DmaCfg<256, 256, 32, 4, 2, 4, 0, 2, 5, 1, 1>;
+
+// Units one XCD can get: at most an eighth of the cost plus one pair, all
+// singles in the worst case.
+__host__ __device__ constexpr int pair_units_per_xcd(int units) {
+  return (units * kPairCost / kNumXcd + kPairCost) / kSingleCost + 1;
+}
+
+template <class CfgP, class CfgS>
+__global__ void __launch_bounds__(CfgP::kThreads)
+    sdd_pair_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
+                    const int32_t* __restrict__ row_token, const int32_t* __restrict__ tokens_per_expert,
+                    const int32_t* __restrict__ padded_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
+                    int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t max_row_blocks,
+                    int32_t apply_gelu) {
+  static_assert(CfgP::kThreads == CfgS::kThreads && CfgP::BN == CfgS::BN, "one workgroup and slice width");
+  static_assert(CfgP::BM == 2 * kBS && CfgS::BM == kBS, "pairs and singles of row blocks");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[max_int(CfgP::kLdsAlloc, CfgS::kLdsAlloc)];
+  // Workgroup bid is XCD bid % 8's tile bid / 8 (units x slices, unit-major).
+  const int32_t first = expert_counts(tokens_per_expert, num_experts, 0);
+  const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
+  const int slices = ffn_dim / CfgP::BN;
+  const int q = static_cast<int>(blockIdx.x) / kNumXcd, xcd = static_cast<int>(blockIdx.x) % kNumXcd;
+  if (q >= pair_units_per_xcd(live_rb) * slices) return;
+  const PairCounts pc = pair_counts(tokens_per_expert, num_experts, first);
+  const UnitsBefore lo =
+      first_pair_unit_at(tokens_per_expert, num_experts, (pc.cost * xcd + kNumXcd - 1) / kNumXcd, first);
+  const UnitsBefore hi = xcd == kNumXcd - 1
+                             ? UnitsBefore{pc.pairs, pc.singles}
+                             : first_pair_unit_at(tokens_per_expert, num_experts,
+                                                  (pc.cost * (xcd + 1) + kNumXcd - 1) / kNumXcd, first);
+  // The XCD's pairs, then its singles (largest first), each unit's slices side by side.
+  const int u = q / slices, slice = q % slices;
+  const int np = hi.pairs - lo.pairs, ns = hi.singles - lo.singles;
+  if (u >= np + ns) return;
+  const bool single = u >= np;
+  const Chunk ch = find_pair_unit(tokens_per_expert, num_experts, single, single ? lo.singles + u - np : lo.pairs + u,
+                                  first);
+  // Not a routing layout (the unit would leave the buffers): skip it.
+  if (ch.expert < 0 || ch.expert >= num_experts || ch.row0 < 0 || ch.rows < 1 ||
+      ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
+    return;
+  const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
+  if (ch.groups == CfgP::BM / 32)
+    sdd_chunk_tile<CfgP>(lds, a, ch, slice * CfgP::BN);
+  else
+    sdd_chunk_tile<CfgS>(lds, a, ch, slice * CfgS::BN);
+}
+
 // ------------------------------------------------------------------ DSD ---
 
 // A: the chunk's rows of H, read in place. All of H is one buffer; lane row
@@ -498,6 +558,18 @@ int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, 
                                        apply_gelu, force, stream);
 }
 
+int launch_sdd_pairs(const void* x, const void* w1, const int32_t* row_token, const int32_t* tokens_per_expert,
+                     const int32_t* padded_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
+                     int64_t num_experts, int64_t max_row_blocks, int32_t apply_gelu, hipStream_t stream) {
+  const int64_t grid = int64_t{kNumXcd} * pair_units_per_xcd(static_cast<int>(max_row_blocks)) * (ffn_dim / SddPairTile::BN);
+  sdd_pair_kernel<SddPairTile, SddNarrowTile><<<static_cast<uint32_t>(grid), SddPairTile::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, tokens_per_expert, padded_offsets,
+      static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens), static_cast<int32_t>(d_model),
+      static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts), static_cast<int32_t>(max_row_blocks),
+      apply_gelu);
+  return check_launch("sdd_experts");
+}
+
 template <class CfgB, int WAVES>
 int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_expert, const int32_t* padded_offsets,
                      const int32_t* row_block_expert, void* out, int64_t max_row_blocks, int64_t num_experts,
@@ -544,15 +616,21 @@ extern "C" int sb_sdd_experts(const void* x, const void* w1, const int32_t* row_
       (max_row_blocks + kNumXcd) * (ffn_dim / kBS) > kI32Max - 65536)
     return fail(SB_ERR_INVALID, "problem too large");
   const int32_t force = expert_gate_override();
-  // The expert tiles are 512 wide; other widths take the per-row-block kernel.
-  // The layer kernel reads x and W1[e] through 32-bit buffer offsets; x of
-  // 2 GiB or more, or one expert's W1 of 2 GiB or more, also go to the
-  // per-row-block kernel, which gathers x with 64-bit addresses. The real
-  // rows are the same bits either way.
+  // The layer kernels read x and W1[e] through 32-bit buffer offsets; x of
+  // 2 GiB or more, or one expert's W1 of 2 GiB or more, go to the
+  // per-row-block kernel, which gathers x with 64-bit addresses, as do
+  // forced row blocks. F % 512 != 0 takes the row-block pairs (256 wide),
+  // other widths the layer kernel (512 wide). The real rows are the same
+  // bits every way.
   const bool offsets_fit = !sdd_wide_x(num_tokens, d_model) && ffn_dim * d_model * 2 < (int64_t{1} << 31);
-  if (ffn_dim % kSddBN != 0 || force == 2 || !offsets_fit)
+  if (force == 2 || !offsets_fit)
     return sb_sdd(x, w1, row_token, row_block_expert, row_offsets, out, num_tokens, d_model, ffn_dim, num_experts,
                   max_row_blocks, apply_gelu, stream);
+  if (ffn_dim % kSddBN != 0) {
+    const int rc = launch_sdd_pairs(x, w1, row_token, tokens_per_expert, padded_offsets, out, num_tokens, d_model,
+                                    ffn_dim, num_experts, max_row_blocks, apply_gelu, as_stream(stream));
+    return rc ? rc : clear_ok();
+  }
   const int rc = dispatch_sdd_layer(x, w1, row_token, row_block_expert, row_offsets, tokens_per_expert, padded_offsets,
                                     out, num_tokens, d_model, ffn_dim, num_experts, max_row_blocks, apply_gelu, force,
                                     as_stream(stream));

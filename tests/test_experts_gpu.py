@@ -74,6 +74,11 @@ CASES = {
     # chunks of every row-group count: odd ones in one row of 8 waves, even
     # ones split between two rows of 4).
     "edges_deep": (lambda s: edge_routing(s), len(EDGE_COUNTS), 512, 8192),
+    # F % 512 != 0: the SDD's row-block pairs (256 x 256 tiles) and singles,
+    # under skew (one expert of many row blocks, odd and even counts) and
+    # with every expert eight row blocks.
+    "pairs768": (lambda s: routing_case("zipf_perm", 4000, 24, seed=s), 24, 256, 768),
+    "uniform768": (lambda s: routing_case("random", 4096, 8, seed=s), 8, 256, 768),
 }
 
 # SDD-only cases (D % 256 != 0 leaves the DSD's layer tiles out): short
@@ -354,6 +359,35 @@ def test_device_choice_follows_the_rule(case: str) -> None:
     if pad:
         dsd_expert = bool(torch.isnan(y[torch.tensor(pad, device="cuda")]).all())
         assert dsd_expert == gate_rule(counts, "dsd", max_rb, d, f, cus)
+
+
+@pytest.mark.parametrize("case", ["zipf130", "skewed", "pairs768", "uniform768"])
+def test_sdd_pairs_write_every_row_of_every_live_row_block(case: str) -> None:
+    # F % 512 != 0: the row-block pairs compute whole row blocks, so a
+    # NaN-filled H comes back with zeros on every padding row, as from the
+    # per-row-block kernel, and either DSD tiling may read it.
+    from sparsebench_amd._lib import check, lib, stream_of
+    from sparsebench_amd.routing import route_device
+
+    idx, x, w1, _ = inputs(case, 5)
+    e, d, f = w1.shape
+    assert f % 512 != 0
+    topo = route_device(idx.cuda(), e, f, 128)
+    max_rb = topo.row_token.numel() // 128
+    fb = f // 128
+    xc, w1c = x.cuda(), w1.cuda()
+    h = torch.full((max_rb * fb, 128, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    check(lib().sb_sdd_experts(
+        xc.data_ptr(), w1c.data_ptr(), topo.row_token.data_ptr(), topo.row_block_expert.data_ptr(),
+        topo.row_offsets.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
+        h.data_ptr(), xc.shape[0], d, f, e, max_rb, 1, stream_of(xc.device)))
+    torch.cuda.synchronize()
+    live = int(topo.padded_offsets[-1])
+    dense = dense_rows(h, fb)
+    assert not torch.isnan(dense[:live]).any(), "every row of every live row block is written"
+    real = torch.zeros(max_rb * 128, dtype=torch.bool, device="cuda")
+    real[torch.as_tensor(real_rows(topo), device="cuda")] = True
+    assert torch.all(dense[:live][~real[:live]] == 0), "padding rows are zeros"
 
 
 def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(monkeypatch) -> None:

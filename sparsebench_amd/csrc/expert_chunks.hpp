@@ -264,7 +264,7 @@ __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __rest
 // per-row-block kernel. Units are numbered in expert order, each expert's
 // pairs before its single. For spreading them over the XCDs a pair costs
 // kPairCost and a single kSingleCost: measured tile times at D = 2048
-// (config 5), 69 and 48 us.
+// (config 5), 69 and 46 us.
 constexpr int kPairCost = 10, kSingleCost = 7;
 
 struct PairCounts {

@@ -10,9 +10,11 @@ A step is one whole layer (routing -> SDD+GELU -> DSD -> combine) replayed
 from a HIP graph captured once, with inputs resident in HBM. Before each
 step a 512 MiB buffer is zeroed (outside the step's events) so the 256 MB
 Infinity Cache and the L2s start cold, as the reference's timing does with
-its L2 flush. Timed: exactly K steps between synchronizations, each bracketed
-by HIP events on the replay stream; ms_per_step is their median and value is
-useful TFLOP/s = 2*2*T*k*D*F / step time (padding FLOPs not counted).
+its L2 flush. Timed: exactly K steps between synchronizations, each as the
+reference's timing loop runs one (sparsebench/timing.py:15-29: flush, event, layer,
+event, synchronize), with the events on the replay stream; ms_per_step is
+their median and value is useful TFLOP/s = 2*2*T*k*D*F / step time (padding
+FLOPs not counted).
 
 Also reported (same JSON line): eager-mode layer time, per-stage times from
 events at the layer's stage marks (each of SDD and DSD is exactly one kernel,
@@ -253,6 +255,7 @@ def main() -> int:
                 s.record(stream)
                 graph.replay()
                 e.record(stream)
+                e.synchronize()  # one step at a time, as the reference's timing loop
                 samples.append((s, e))
         torch.cuda.synchronize()
         return [s.elapsed_time(e) for s, e in samples]

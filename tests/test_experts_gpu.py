@@ -79,6 +79,8 @@ CASES = {
     # with every expert eight row blocks.
     "pairs768": (lambda s: routing_case("zipf_perm", 4000, 24, seed=s), 24, 256, 768),
     "uniform768": (lambda s: routing_case("random", 4096, 8, seed=s), 8, 256, 768),
+    # One expert of 3000 rows (24 row blocks: 12 pairs), F = 768.
+    "one_expert768": (lambda s: torch.zeros(3000, 1, dtype=torch.int64), 1, 256, 768),
 }
 
 # SDD-only cases (D % 256 != 0 leaves the DSD's layer tiles out): short
@@ -209,7 +211,7 @@ def test_dsd_experts_padding_rows_do_not_reach_real_rows(monkeypatch, gate: str)
 
 
 @pytest.mark.parametrize("gate", GATES)
-@pytest.mark.parametrize("case", ["uniform64", "zipf130", "edges", "skewed", "edges_deep"])
+@pytest.mark.parametrize("case", ["uniform64", "zipf130", "edges", "skewed", "edges_deep", "pairs768"])
 def test_moe_forward_expert_tiles_bit_identical(monkeypatch, case: str, gate: str) -> None:
     from sparsebench_amd.moe import moe_forward
 
@@ -361,7 +363,7 @@ def test_device_choice_follows_the_rule(case: str) -> None:
         assert dsd_expert == gate_rule(counts, "dsd", max_rb, d, f, cus)
 
 
-@pytest.mark.parametrize("case", ["zipf130", "skewed", "pairs768", "uniform768"])
+@pytest.mark.parametrize("case", ["zipf130", "skewed", "pairs768", "uniform768", "one_expert768"])
 def test_sdd_pairs_write_every_row_of_every_live_row_block(case: str) -> None:
     # F % 512 != 0: the row-block pairs compute whole row blocks, so a
     # NaN-filled H comes back with zeros on every padding row, as from the

@@ -101,6 +101,11 @@ __device__ __forceinline__ int32_t expert_counts(const int32_t* __restrict__ tok
   return n;
 }
 
+// The helpers below take `first`, the counts of the first pass
+// (expert_counts(tokens_per_expert, num_experts, 0)), loaded once by the
+// kernel; they load only the passes after it. Rebuilding the first pass's
+// vector in every helper cost 64 v_writelane_b32 and a wait on the scalar
+// loads each time.
 struct Chunk {
   int32_t expert;  // -1: no such chunk
   int32_t row0;    // first padded row (a multiple of 128)
@@ -117,12 +122,13 @@ __device__ __forceinline__ int32_t padded_rows(int32_t n) { return n > 0 ? (n + 
 // before it (padded_offsets[e] of the routing layout), computed here from the
 // counts instead of loaded: one dependent load less before the tile's first.
 template <int RMAX>
-__device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts, int c) {
+__device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts, int c,
+                                            int32_t first) {
   Chunk ch{-1, 0, 0, 0};
   int before = 0;       // chunks of the experts before this pass
   int rows_before = 0;  // padded rows of the experts before this pass
   for (int base = 0; base < num_experts; base += 64) {
-    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
     const int cc = Chunking<RMAX>::count(n);
     const int incl = wave_inclusive_scan(cc);
     const int pincl = wave_inclusive_scan(padded_rows(n));
@@ -157,12 +163,12 @@ __device__ __forceinline__ Chunk find_chunk(const int32_t* __restrict__ tokens_p
 // mask is set. One pass over the counts.
 template <int RMAX>
 __device__ __forceinline__ uint32_t big_chunks_of_group(const int32_t* __restrict__ tokens_per_expert,
-                                                        int32_t num_experts, int g0, int G) {
+                                                        int32_t num_experts, int g0, int G, int32_t first) {
   constexpr int kFull = Chunking<RMAX>::kRows / 32;
   uint32_t mask = 0;
   int before = 0;
   for (int base = 0; base < num_experts && before < g0 + G; base += 64) {
-    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
     const int c = Chunking<RMAX>::count(n);
     const int incl = wave_inclusive_scan(c);
     const int last = before + incl - 1;  // this expert's last chunk
@@ -201,12 +207,12 @@ __device__ __forceinline__ void lpt_group_tile(int local, int G, int slices, uin
 // one ballot per g and pass (every wave computes the same values).
 template <int RMAX>
 __device__ __forceinline__ void single_chunk_hist(const int32_t* __restrict__ tokens_per_expert, int32_t num_experts,
-                                                  int32_t (&hist)[RMAX + 1]) {
+                                                  int32_t first, int32_t (&hist)[RMAX + 1]) {
 #pragma unroll
   for (int g = 0; g <= RMAX; ++g) hist[g] = 0;
 #pragma unroll 1
   for (int base = 0; base < num_experts; base += 64) {
-    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
     const int groups = n > 0 ? (n + 31) / 32 : 0;
 #pragma unroll
     for (int g = 1; g <= RMAX; ++g) hist[g] += __builtin_popcountll(__ballot(groups == g));
@@ -220,7 +226,7 @@ __device__ __forceinline__ void single_chunk_hist(const int32_t* __restrict__ to
 // routing layout), computed from the counts.
 template <int RMAX>
 __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __restrict__ tokens_per_expert,
-                                                           int32_t num_experts, int k,
+                                                           int32_t num_experts, int k, int32_t first,
                                                            const int32_t (&hist)[RMAX + 1]) {
   Chunk ch{-1, 0, 0, 0};
   int g = RMAX;
@@ -231,7 +237,7 @@ __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __rest
   if (g < 1) return ch;
   int rows_before = 0;  // padded rows of the experts before this pass
   for (int base = 0; base < num_experts; base += 64) {
-    const int32_t n = expert_counts(tokens_per_expert, num_experts, base);
+    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
     const uint64_t match = __ballot(n > 0 && (n + 31) / 32 == g);
     const int cnt = __builtin_popcountll(match);
     if (k < cnt) {

@@ -251,8 +251,8 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     int rank, slice;
     if (!balanced_chunk_tile(static_cast<int>(blockIdx.x), chunks, slices, &rank, &slice)) return;
     int32_t hist[kSddRmax + 1];
-    single_chunk_hist<kSddRmax>(tokens_per_expert, num_experts, hist);
-    ch = find_single_chunk_by_size<kSddRmax>(tokens_per_expert, num_experts, rank, hist);
+    single_chunk_hist<kSddRmax>(tokens_per_expert, num_experts, first, hist);
+    ch = find_single_chunk_by_size<kSddRmax>(tokens_per_expert, num_experts, rank, first, hist);
     n0_slice = slice;
   } else {
     // Groups of `group` chunks x slices (tile_coords), largest chunks first
@@ -262,10 +262,10 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     const int per_group = group * slices;
     const int g0 = (tile / per_group) * group;
     const int G = min(group, chunks - g0);
-    const uint32_t big = big_chunks_of_group<kSddRmax>(tokens_per_expert, num_experts, g0, G);
+    const uint32_t big = big_chunks_of_group<kSddRmax>(tokens_per_expert, num_experts, g0, G, first);
     int pos, slice;
     lpt_group_tile(tile - (g0 / group) * per_group, G, slices, big, &pos, &slice);
-    ch = find_chunk<kSddRmax>(tokens_per_expert, num_experts, __builtin_amdgcn_readfirstlane(g0 + pos));
+    ch = find_chunk<kSddRmax>(tokens_per_expert, num_experts, __builtin_amdgcn_readfirstlane(g0 + pos), first);
     n0_slice = __builtin_amdgcn_readfirstlane(slice);
   }
   // Not a routing layout (the chunk would leave the buffers): skip it.
@@ -460,7 +460,7 @@ __global__ void __launch_bounds__(64 * WAVES)
   int c, slice;
   tile_coords(tile, chunks, slices, group, &c, &slice);
   if (c >= chunks) return;
-  const Chunk ch = find_chunk<kRmax>(tokens_per_expert, num_experts, c);
+  const Chunk ch = find_chunk<kRmax>(tokens_per_expert, num_experts, c, first);
   if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kRmax ||
       ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
     return;

@@ -469,8 +469,11 @@ __device__ __forceinline__ bool expert_tiles_chosen(const LayoutSummary& sum, in
   if (gate == kGateSdd) {
     // Rounds of 512-wide tiles over the CUs: large experts take the expert
     // chunks when these need fewer rounds than the row blocks.
-    const int64_t chunk_rounds = (static_cast<int64_t>(sum.chunks_a) * slices + cus - 1) / cus;
-    const int64_t block_rounds = (static_cast<int64_t>(sum.chunks_b) * slices + cus - 1) / cus;
+    // 32-bit: the host bounds live row blocks x slices below 2^31 (a 64-bit
+    // division is a long scalar sequence at every tile's start).
+    const uint32_t c = static_cast<uint32_t>(cus);
+    const uint32_t chunk_rounds = (static_cast<uint32_t>(sum.chunks_a) * static_cast<uint32_t>(slices) + c - 1) / c;
+    const uint32_t block_rounds = (static_cast<uint32_t>(sum.chunks_b) * static_cast<uint32_t>(slices) + c - 1) / c;
     chosen = balanced && (sum.rows <= static_cast<int64_t>(256) * num_experts || chunk_rounds < block_rounds);
   }
   return __builtin_amdgcn_readfirstlane(chosen ? 1 : 0) != 0;

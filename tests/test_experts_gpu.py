@@ -81,6 +81,8 @@ CASES = {
     "uniform768": (lambda s: routing_case("random", 4096, 8, seed=s), 8, 256, 768),
     # One expert of 3000 rows (24 row blocks: 12 pairs), F = 768.
     "one_expert768": (lambda s: torch.zeros(3000, 1, dtype=torch.int64), 1, 256, 768),
+    # Five tokens over three experts at F = 768 (singles only, a grid of a few workgroups).
+    "tiny768": (lambda s: torch.tensor([[0], [2], [2], [0], [2]], dtype=torch.int64), 3, 256, 768),
 }
 
 # SDD-only cases (D % 256 != 0 leaves the DSD's layer tiles out): short
@@ -363,7 +365,7 @@ def test_device_choice_follows_the_rule(case: str) -> None:
         assert dsd_expert == gate_rule(counts, "dsd", max_rb, d, f, cus)
 
 
-@pytest.mark.parametrize("case", ["zipf130", "skewed", "pairs768", "uniform768", "one_expert768"])
+@pytest.mark.parametrize("case", ["zipf130", "skewed", "pairs768", "uniform768", "one_expert768", "tiny768"])
 def test_sdd_pairs_write_every_row_of_every_live_row_block(case: str) -> None:
     # F % 512 != 0: the row-block pairs compute whole row blocks, so a
     # NaN-filled H comes back with zeros on every padding row, as from the

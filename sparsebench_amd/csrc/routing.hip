@@ -264,6 +264,12 @@ __global__ void __launch_bounds__(kChunk)
   const bool placing = static_cast<int32_t>(blockIdx.x) < num_chunks;
   const int own = placing ? static_cast<int>(blockIdx.x) : num_chunks;
   const int64_t stride = num_experts + 1;
+  // This lane's copy, read before the column sums so that its load waits
+  // alongside theirs rather than after the scan.
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kChunk + tid;
+  bool bad = false;
+  int32_t token = -1;
+  const int32_t e = placing ? read_expert(idx, c, n, tokens, num_experts, valid_tokens, &bad, &token) : -1;
 
   // Column tid (expert tid): all of its at most kScanChunks loads are issued
   // before the first is used, so they are in flight together.
@@ -302,10 +308,6 @@ __global__ void __launch_bounds__(kChunk)
     for (int i = tid; i < kWaves * num_experts; i += kChunk) wave_counts[i] = 0;
     __syncthreads();
     const int wave = tid >> 6;
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * kChunk + tid;
-    bool bad;
-    int32_t token;
-    const int32_t e = read_expert(idx, c, n, tokens, num_experts, valid_tokens, &bad, &token);
     const bool valid = e >= 0;
     const uint64_t peers = same_expert_lanes(valid, e, num_bits);
     const uint64_t lower = peers & lanes_below();

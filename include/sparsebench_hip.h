@@ -36,6 +36,16 @@ const char* sb_last_error(void);
 /* Library version, for a binder to check it loaded the right file. */
 int32_t sb_version(void);
 
+/* No counterpart in the reference: test hooks, process-wide overrides of a
+ * choice the library otherwise makes itself (value 0 restores the choice).
+ * For tests that must reach each code path; outputs do not depend on them.
+ *   SB_HOOK_EXPERT_GATE  1: the layer kernels' expert tiles, 2: row blocks
+ *   SB_HOOK_TOPK_KERNEL  1: the top-k router's wave form, 2: its lane form */
+#define SB_HOOK_EXPERT_GATE 0
+#define SB_HOOK_TOPK_KERNEL 1
+#define SB_NUM_TEST_HOOKS 2
+int sb_set_test_hook(int32_t hook, int32_t value);
+
 /* Replaces arch_probe (csrc/smoke.cu:23-38, csrc/ops.hpp:11).
  * Writes the architecture number of the code that ran (950 on gfx950)
  * into out[0..n). n must be positive. */

@@ -45,6 +45,18 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_TEST_HOOKS = {"expert_gate": 0, "topk_kernel": 1}
+
+
+def set_test_hook(name: str, value: int) -> None:
+    """Forces one of the library's own choices for tests (include/sparsebench_hip.h:
+    expert_gate 1 = expert tiles, 2 = row blocks; topk_kernel 1 = wave form,
+    2 = lane form); 0 restores the choice."""
+    if name not in _TEST_HOOKS:
+        raise ValueError(f"unknown test hook {name!r}")
+    check(lib().sb_set_test_hook(_TEST_HOOKS[name], int(value)))
+
+
 def arch_probe(n: int) -> torch.Tensor:
     """int32[n] filled with the architecture number of the code that ran (950 on gfx950)."""
     if n <= 0:

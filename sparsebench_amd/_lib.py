@@ -24,6 +24,7 @@ _ptr = ctypes.c_void_p
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sb_last_error": (ctypes.c_char_p, []),
     "sb_version": (_i32, []),
+    "sb_set_test_hook": (_c_int, [_i32, _i32]),
     "sb_arch_probe": (_c_int, [_ptr, _i64, _ptr]),
     "sb_routing_sizes": (
         _c_int,

@@ -35,13 +35,11 @@ inline int check_launch(const char* what) {
   return SB_OK;
 }
 
-// Test hook read from the environment on each call (0 when unset, which
-// keeps the built-in choice): SPARSEBENCH_EXPERT_GATE forces one tiling of
-// the layer kernels, SPARSEBENCH_TOPK_KERNEL one form of the top-k router.
-inline int env_override(const char* name) {
-  const char* v = std::getenv(name);
-  return v ? std::atoi(v) : 0;
-}
+// Test hooks (sb_set_test_hook): process-wide overrides of a built-in
+// choice, 0 keeping the choice. SB_HOOK_EXPERT_GATE forces one tiling of
+// the layer kernels, SB_HOOK_TOPK_KERNEL one form of the top-k router.
+// Only tests set them; the product path reads no environment.
+int32_t test_hook(int32_t hook);
 
 // Row blocks per tile group (see tile_coords).
 constexpr int kTileGroup = 8;

@@ -479,10 +479,10 @@ __device__ __forceinline__ bool expert_tiles_chosen(const LayoutSummary& sum, in
   return __builtin_amdgcn_readfirstlane(chosen ? 1 : 0) != 0;
 }
 
-// Host side of the gate: SPARSEBENCH_EXPERT_GATE=1 forces the expert
-// tiles, 2 the row blocks (for tests and tuning); 0 or unset chooses.
+// Host side of the gate: the test hook SB_HOOK_EXPERT_GATE = 1 forces the
+// expert tiles, 2 the row blocks; 0 (its default) chooses.
 inline int32_t expert_gate_override() {
-  const int v = env_override("SPARSEBENCH_EXPERT_GATE");
+  const int32_t v = test_hook(SB_HOOK_EXPERT_GATE);
   return v == 1 || v == 2 ? v : 0;
 }
 

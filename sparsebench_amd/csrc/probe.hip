@@ -1,4 +1,7 @@
-// arch_probe (the reference's csrc/smoke.cu) and the library's error state.
+// arch_probe (the reference's csrc/smoke.cu), the library's error state and
+// its test hooks.
+
+#include <atomic>
 
 #include "common.hpp"
 
@@ -7,6 +10,14 @@ namespace sb {
 std::string& last_error() {
   thread_local std::string msg;
   return msg;
+}
+
+namespace {
+std::atomic<int32_t> g_test_hooks[SB_NUM_TEST_HOOKS];
+}  // namespace
+
+int32_t test_hook(int32_t hook) {
+  return hook >= 0 && hook < SB_NUM_TEST_HOOKS ? g_test_hooks[hook].load(std::memory_order_relaxed) : 0;
 }
 
 int fail(int code, const char* fmt, ...) {
@@ -42,6 +53,12 @@ using namespace sb;
 extern "C" const char* sb_last_error(void) { return last_error().c_str(); }
 
 extern "C" int32_t sb_version(void) { return 1; }
+
+extern "C" int sb_set_test_hook(int32_t hook, int32_t value) {
+  if (hook < 0 || hook >= SB_NUM_TEST_HOOKS) return fail(SB_ERR_INVALID, "unknown test hook %d", hook);
+  g_test_hooks[hook].store(value, std::memory_order_relaxed);
+  return clear_ok();
+}
 
 extern "C" int sb_arch_probe(int32_t* out, int64_t n, void* stream) {
   if (n <= 0) return fail(SB_ERR_INVALID, "arch_probe: n must be positive, got %lld", static_cast<long long>(n));

@@ -1,6 +1,6 @@
 // Router side of the MoE layer on gfx950: plain top-k and token rounding
 // (the reference's sparsebench/token_rounding.py: top_k_assignments at
-// 42-49, round_counts at 52-58, token_rounding at 61-85), with the rounding
+// 39-46, round_counts at 49-55, token_rounding at 58-81), with the rounding
 // fused into routing: scores go in, and out come the assignment list and
 // the block-sparse layout that SDD / DSD / the assigned combine consume,
 // with no host sync (the reference needs one, for nonzero()).
@@ -673,9 +673,10 @@ int launch_topk(const float* scores, int64_t num_tokens, int32_t num_experts, in
   const uint32_t groups = static_cast<uint32_t>((num_tokens + kTopkTokensPerGroup - 1) / kTopkTokensPerGroup);
   const int per = (num_experts + 63) / 64;
   // A lane per token unless its insertion work (E x the rounded-up k) is
-  // large; SPARSEBENCH_TOPK_KERNEL=1 forces the wave form, 2 the lane form.
+  // large; the test hook SB_HOOK_TOPK_KERNEL = 1 forces the wave form, 2
+  // the lane form.
   const int kmax = k <= 1 ? 1 : k <= 2 ? 2 : k <= 4 ? 4 : k <= 8 ? 8 : 16;
-  const int forced = env_override("SPARSEBENCH_TOPK_KERNEL");
+  const int forced = test_hook(SB_HOOK_TOPK_KERNEL);
   if (forced == 2 || (forced != 1 && kmax * num_experts <= 2048)) {
 #define SB_TOPK_LANE(K) \
   router_topk_lane_kernel<K><<<groups, 64, 0, s>>>(scores, num_tokens, num_experts, k, shifted, chunk_counts, top_idx, top_weight)

@@ -10,7 +10,6 @@ real size from padded_offsets / row_offsets on the GPU.
 
 from __future__ import annotations
 
-import os
 from collections.abc import Callable
 
 import torch
@@ -21,17 +20,34 @@ from sparsebench_amd.spmm import dsd, sdd
 BLOCK_SIZE = 128
 STAGES = ("routing", "SDD + GELU (fused)", "DSD", "combine")
 
+# The stage kernels the layer runs; every choice gives the same output bits.
+#   expert_tiles   SDD / DSD on the layer kernels (sdd_experts_cuda /
+#                  dsd_experts_cuda), else the per-row-block sdd / dsd.
+_STAGE_OPTIONS = {"expert_tiles": True}
+
+
+def set_stage_options(**options: bool) -> dict[str, bool]:
+    """Sets the layer's stage choices (keys of _STAGE_OPTIONS) for this
+    process and returns the previous values. For tests and measurements:
+    outputs do not depend on them."""
+    unknown = set(options) - set(_STAGE_OPTIONS)
+    if unknown:
+        raise ValueError(f"unknown stage options {sorted(unknown)}")
+    previous = dict(_STAGE_OPTIONS)
+    _STAGE_OPTIONS.update({k: bool(v) for k, v in options.items()})
+    return previous
+
 
 def _no_mark(stage: str) -> None:
     pass
 
 
 def _expert_tiles(topo, d_model: int, ffn_dim: int) -> bool:
-    """SDD / DSD on expert-major tiles (the default), unless
-    SPARSEBENCH_EXPERT_TILES=0 or the shape needs the per-row-block kernels."""
+    """SDD / DSD on the layer kernels (the default), unless switched off or
+    the shape needs the per-row-block kernels."""
     from sparsebench_amd import _C
 
-    if os.environ.get("SPARSEBENCH_EXPERT_TILES", "1") == "0":
+    if not _STAGE_OPTIONS["expert_tiles"]:
         return False
     return _C.expert_tiles_fit(d_model, ffn_dim, topo.row_token.numel() // topo.block_size)
 

@@ -67,16 +67,16 @@ def test_top_k_assignments_exact(name, t, e, k, tile) -> None:
     assert torch.equal(got.weight.cpu(), torch.from_numpy(ref.weight))
 
 
-@pytest.mark.parametrize("kernel", ["1", "2"])  # SPARSEBENCH_TOPK_KERNEL: 1 = a wave per token, 2 = a lane per token
+@pytest.mark.parametrize("kernel", ["1", "2"])  # the top-k test hook: 1 = a wave per token, 2 = a lane per token
 @pytest.mark.parametrize(("name", "t", "e", "k", "tile"), [("ties5", 300, 6, 2, 8), ("ties3", 129, 70, 2, 4),
                                                           ("uniform", 1000, 65, 3, 16), ("ties4", 700, 37, 5, 8),
                                                           ("zipf", 500, 1000, 16, 32), ("uniform", 333, 200, 9, 16)])
-def test_both_top_k_forms_exact(kernel, name, t, e, k, tile, monkeypatch) -> None:
+def test_both_top_k_forms_exact(kernel, name, t, e, k, tile, hooks) -> None:
     # The top-k kernel is chosen by E x k; each form, forced, must give the
     # oracle's list and the oracle's token rounding.
     from sparsebench_amd.token_rounding import token_rounding, top_k_assignments
 
-    monkeypatch.setenv("SPARSEBENCH_TOPK_KERNEL", kernel)
+    hooks.topk_kernel(kernel)
     scores = scores_of(name, t, e)
     got = top_k_assignments(scores.cuda(), k)
     ref = topk_ref(scores.numpy(), k)

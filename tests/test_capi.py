@@ -159,3 +159,13 @@ def test_assigned_entry_points_reject(lib) -> None:
     assert "weight dtype" in _err(lib)
     assert lib.sb_combine_assigned(p, p, p, 2, p, None, p, 1, 12, 4, None, None) == 1
     assert "multiple of 8" in _err(lib)
+
+
+def test_test_hooks_set_and_reject(lib) -> None:
+    assert lib.sb_set_test_hook(0, 1) == 0
+    assert lib.sb_set_test_hook(0, 0) == 0
+    assert lib.sb_set_test_hook(1, 0) == 0
+    assert lib.sb_set_test_hook(2, 1) == 1
+    assert "unknown test hook" in _err(lib)
+    assert lib.sb_set_test_hook(-1, 1) == 1
+

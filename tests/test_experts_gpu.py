@@ -3,8 +3,8 @@ against the per-row-block kernels and the oracle.
 
 Each entry point launches one kernel whose workgroups choose, on the GPU,
 between expert-chunk tiles and row-block tiles (the expert tiles when the
-routing is balanced). SPARSEBENCH_EXPERT_GATE=1 / 2 forces one side, so
-both are tested on every routing here, and 0 (unset) tests the choice.
+routing is balanced). The expert_gate test hook (1 / 2) forces one side,
+so both are tested on every routing here, and 0 tests the choice.
 
 Every real row of H and of y must equal, bit for bit, what sdd_cuda /
 dsd_cuda write for it: both accumulate each output in fp32 over K in the same
@@ -137,12 +137,12 @@ def inputs(case: str, seed: int):
 
 @pytest.mark.parametrize("gate", GATES)
 @pytest.mark.parametrize("case", list(CASES) + list(SDD_CASES))
-def test_sdd_experts_rows_equal_row_block_kernel(monkeypatch, gate: str, case: str) -> None:
+def test_sdd_experts_rows_equal_row_block_kernel(hooks, gate: str, case: str) -> None:
     from sparsebench_amd import _C
     from sparsebench_amd.routing import route_device
     from sparsebench_amd.spmm import sdd
 
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    hooks.expert_gate(gate)
     idx, x, w1, _ = inputs(case, int(gate))
     e, _, f = w1.shape
     topo = route_device(idx.cuda(), e, f, 128)
@@ -163,12 +163,12 @@ def test_sdd_experts_rows_equal_row_block_kernel(monkeypatch, gate: str, case: s
 
 @pytest.mark.parametrize("gate", GATES)
 @pytest.mark.parametrize("case", list(CASES))
-def test_dsd_experts_rows_equal_row_block_kernel(monkeypatch, case: str, gate: str) -> None:
+def test_dsd_experts_rows_equal_row_block_kernel(hooks, case: str, gate: str) -> None:
     from sparsebench_amd import _C
     from sparsebench_amd.routing import route_device
     from sparsebench_amd.spmm import dsd, sdd
 
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    hooks.expert_gate(gate)
     idx, x, w1, w2 = inputs(case, 10 + int(gate))
     e, d, f = w1.shape
     topo = route_device(idx.cuda(), e, f, 128)
@@ -186,7 +186,7 @@ def test_dsd_experts_rows_equal_row_block_kernel(monkeypatch, case: str, gate: s
 
 
 @pytest.mark.parametrize("gate", GATES)
-def test_dsd_experts_padding_rows_do_not_reach_real_rows(monkeypatch, gate: str) -> None:
+def test_dsd_experts_padding_rows_do_not_reach_real_rows(hooks, gate: str) -> None:
     # Padding rows of H may hold anything (the expert SDD leaves some
     # unwritten): the expert tiling does not read them, the row-block one
     # reads them into padding rows of y only, which it does not write.
@@ -194,7 +194,7 @@ def test_dsd_experts_padding_rows_do_not_reach_real_rows(monkeypatch, gate: str)
     from sparsebench_amd.routing import route_device
     from sparsebench_amd.spmm import sdd
 
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    hooks.expert_gate(gate)
     idx, x, w1, w2 = inputs("edges", 3)
     e, d, f = w1.shape
     topo = route_device(idx.cuda(), e, f, 128)
@@ -214,24 +214,24 @@ def test_dsd_experts_padding_rows_do_not_reach_real_rows(monkeypatch, gate: str)
 
 @pytest.mark.parametrize("gate", GATES)
 @pytest.mark.parametrize("case", ["uniform64", "zipf130", "edges", "skewed", "edges_deep", "pairs768"])
-def test_moe_forward_expert_tiles_bit_identical(monkeypatch, case: str, gate: str) -> None:
+def test_moe_forward_expert_tiles_bit_identical(hooks, case: str, gate: str) -> None:
     from sparsebench_amd.moe import moe_forward
 
     idx, x, w1, w2 = inputs(case, 21)
     g = torch.Generator().manual_seed(5)
     gates = torch.softmax(torch.randn(idx.shape, generator=g), dim=-1).bfloat16().cuda()
     args = (x.cuda(), idx.cuda(), gates, w1.cuda(), w2.cuda())
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    hooks.stage(expert_tiles=False)
     ref = moe_forward(*args)
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    hooks.stage(expert_tiles=True)
+    hooks.expert_gate(gate)
     assert torch.equal(moe_forward(*args), ref)
 
 
 @pytest.mark.parametrize(("config", "routing"),
                          [("fine_grained", "random"), ("fine_grained", "zipf_perm"), ("mixtral", "random"),
                           ("replay_sweep", "zipf_perm")])
-def test_full_size_layer_is_the_same_for_every_tiling(monkeypatch, config: str, routing: str) -> None:
+def test_full_size_layer_is_the_same_for_every_tiling(hooks, config: str, routing: str) -> None:
     # The benchmark configurations at their real sizes (the bench's inputs):
     # the layer with the per-row-block kernels, with the device's choice,
     # and with each tiling forced gives the same bits.
@@ -240,17 +240,17 @@ def test_full_size_layer_is_the_same_for_every_tiling(monkeypatch, config: str, 
 
     x, idx, gates, w1, w2 = make_layer(SHAPES[config], routing, seed=0)
     gates = gates.bfloat16()
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    hooks.stage(expert_tiles=False)
     ref = moe_forward(x, idx, gates, w1, w2)
     assert torch.isfinite(ref.float()).all()
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
+    hooks.stage(expert_tiles=True)
     for gate in GATES:
-        monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+        hooks.expert_gate(gate)
         assert torch.equal(moe_forward(x, idx, gates, w1, w2), ref), f"gate {gate}"
 
 
 @pytest.mark.parametrize("gate", GATES)
-def test_moe_forward_rounded_expert_tiles_bit_identical(monkeypatch, gate: str) -> None:
+def test_moe_forward_rounded_expert_tiles_bit_identical(hooks, gate: str) -> None:
     from sparsebench_amd.moe import moe_forward_rounded
     from sparsebench_amd.workloads import router_scores
 
@@ -260,10 +260,10 @@ def test_moe_forward_rounded_expert_tiles_bit_identical(monkeypatch, gate: str) 
     x = torch.randn(t, d, generator=g).bfloat16().cuda()
     w1 = (torch.randn(e, d, f, generator=g) / math.sqrt(d)).bfloat16().cuda()
     w2 = (torch.randn(e, f, d, generator=g) / math.sqrt(f)).bfloat16().cuda()
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    hooks.stage(expert_tiles=False)
     ref = moe_forward_rounded(x, scores, 2, w1, w2)
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_GATE", gate)
+    hooks.stage(expert_tiles=True)
+    hooks.expert_gate(gate)
     assert torch.equal(moe_forward_rounded(x, scores, 2, w1, w2), ref)
 
 
@@ -394,7 +394,7 @@ def test_sdd_pairs_write_every_row_of_every_live_row_block(case: str) -> None:
     assert torch.all(dense[:live][~real[:live]] == 0), "padding rows are zeros"
 
 
-def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(monkeypatch) -> None:
+def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(hooks) -> None:
     # 130 experts with 2 rows each (balanced), D = 2048: the DSD's 130 x 8
     # expert tiles exceed its grid (1024 workgroups on 256 CUs), so it runs
     # row blocks, and the SDD must then run row blocks too, writing every
@@ -417,7 +417,7 @@ def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(mon
     counts = topo.tokens_per_expert.cpu().tolist()
     assert dsd_chunks(counts, f) * (d // 256) > dsd_grid(max_rb, e, d)
     assert not gate_rule(counts, "sdd", max_rb, d, f) and not gate_rule(counts, "dsd", max_rb, d, f)
-    monkeypatch.delenv("SPARSEBENCH_EXPERT_GATE", raising=False)
+    hooks.expert_gate(0)
     fb = f // 128
     h = torch.full((max_rb * fb, 128, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
     check(lib().sb_sdd_experts(
@@ -428,7 +428,7 @@ def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(mon
     live = int(topo.padded_offsets[-1])
     assert not torch.isnan(dense_rows(h, fb)[:live]).any(), "every row of every live row block is written"
     gates = torch.ones(t, 1, device="cuda")
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "0")
+    hooks.stage(expert_tiles=False)
     ref = moe_forward(x, idx, gates, w1, w2)
-    monkeypatch.setenv("SPARSEBENCH_EXPERT_TILES", "1")
+    hooks.stage(expert_tiles=True)
     assert torch.equal(moe_forward(x, idx, gates, w1, w2), ref)

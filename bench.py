@@ -301,27 +301,34 @@ def main() -> int:
         print(f"[bench] eager: {eager_ms} ms, stages {stages}", flush=True)
 
     # ---- roofline of the dominant kernel (SDD or DSD, one kernel each) ----
+    # Both matmul stages are reported; the top-level fields are the longer one's.
     nbytes = algorithmic_bytes(shape, active)
     roofline = None
     if stages:
-        sdd_ms, dsd_ms = stages["SDD + GELU (fused)"], stages["DSD"]
-        name, kms = ("sdd", sdd_ms) if sdd_ms >= dsd_ms else ("dsd", dsd_ms)
         flops = shape.useful_flops // 2
-        ai = flops / nbytes[name]
-        hbm_bound = ai < MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
-        if hbm_bound:
-            achieved = nbytes[name] / (kms * 1e-3) / 1e9
-            roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4),
-                        "traffic": measured_traffic(args.config, args.routing, name), "kernel": f"{name} stage (one kernel)",
-                        "algorithmic_bytes": nbytes[name], "kernel_ms": kms,
+
+        def stage_roofline(name: str, kms: float) -> dict:
+            ai = flops / nbytes[name]
+            traffic = measured_traffic(args.config, args.routing, name)
+            entry = {"kernel": f"{name} stage (one kernel)", "kernel_ms": kms, "traffic": traffic,
+                     "traffic_source": (f"profiles/traffic_*.md (rocprofv3 FETCH_SIZE / WRITE_SIZE of this bench "
+                                        f"command, committed; not measured in this run)" if traffic is not None
+                                        else None)}
+            if ai < MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+                achieved = nbytes[name] / (kms * 1e-3) / 1e9
+                return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), **entry, "algorithmic_bytes": nbytes[name],
                         "useful_tflops": round(flops / (kms * 1e-3) / 1e12, 2)}
-        else:
             achieved = flops / (kms * 1e-3) / 1e12
-            roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                        "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                        "traffic": measured_traffic(args.config, args.routing, name),
-                        "kernel": f"{name} stage (one kernel)", "useful_flops": flops, "kernel_ms": kms}
+            return {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), **entry, "useful_flops": flops}
+
+        per_kernel = {"sdd": stage_roofline("sdd", stages["SDD + GELU (fused)"]),
+                      "dsd": stage_roofline("dsd", stages["DSD"])}
+        name = "sdd" if per_kernel["sdd"]["kernel_ms"] >= per_kernel["dsd"]["kernel_ms"] else "dsd"
+        roofline = dict(per_kernel[name])
+        roofline["stages"] = {k: {f: v[f] for f in ("bound", "achieved", "unit", "frac", "kernel_ms", "traffic")}
+                              for k, v in per_kernel.items()}
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -81,8 +81,9 @@ int sb_routing(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, i
  * `workspace`: the per-chunk counts live in a fixed device array of
  * 524288 int32 (2 MiB) that each GPU holds until the process ends. Problems
  * that need more scratch (ceil(T*k / 1024) * (E + 1) int32, from
- * sb_routing_sizes) are rejected with SB_ERR_INVALID. The first call on a
- * device looks up that device's array (make it outside graph capture);
+ * sb_routing_sizes) are rejected with SB_ERR_INVALID. The array used is
+ * that of the stream's device (the current device for the null stream);
+ * the first call on a device looks it up (make it outside graph capture);
  * no call allocates. Calls that overlap on one GPU share the array and
  * race: issue them on one stream. */
 int sb_routing_noalloc(const void* expert_idx, int32_t idx_is_i64, int64_t num_tokens, int32_t k,

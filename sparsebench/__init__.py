@@ -8,6 +8,12 @@ setup.py:14, csrc/bindings.cpp:5). Each of those names is the module of
 package: `sparsebench.moe is sparsebench_amd.moe`, so there is one copy of
 every module and patching one name patches both.
 
+Only the forward path's modules are registered (_MODULES). The reference's
+benchmark and test support modules (sparsebench.reference, .timing,
+.baselines) and the CPU functions of its sparsebench.topology
+(build_topology, bsr_to_dense, dense_to_bsr) are not part of this build and
+raise ImportError / AttributeError here.
+
 Importing this package does not load the HIP library; that happens on the
 first op call, as in `sparsebench_amd`.
 """

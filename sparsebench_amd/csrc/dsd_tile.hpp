@@ -12,6 +12,8 @@ namespace sb {
 template <class Cfg>
 struct DsdDmaSrc {
   static constexpr int kStepsPerBlock = Cfg::BM / Cfg::BK;
+  // A row block's reduction is whole blocks (reduction_fits for any count).
+  static_assert(!Cfg::APAIR || kStepsPerBlock % 2 == 0, "paired A needs an even step count per block");
   const uint16_t* blocks;
   const uint16_t* w;
   const int32_t* col_indices;

@@ -528,6 +528,10 @@ int launch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, co
   // Both tilings have at most max_row_blocks x F/512 tiles (every chunk
   // starts a row block of its own).
   static_assert(CfgB::BN == kSddBN, "one grid for both tilings");
+  if (!reduction_fits<CfgB>(d_model) || !reduction_fits<SddHalfTile>(d_model) ||
+      !reduction_fits<ChunkCfg<4, kSddBN, kSddWaves, 4>>(d_model))
+    return fail(SB_ERR_INVALID, "sdd_experts: D (%lld) is not a whole number of the tiles' K steps",
+                static_cast<long long>(d_model));
   const int64_t tiles = max_row_blocks * (ffn_dim / kSddBN);
   int64_t dsd_grid = 0;  // no DSD expert tiles for D % 256 != 0
   if (d_model % kDsdBN == 0)
@@ -561,6 +565,9 @@ int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, 
 int launch_sdd_pairs(const void* x, const void* w1, const int32_t* row_token, const int32_t* tokens_per_expert,
                      const int32_t* padded_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
                      int64_t num_experts, int64_t max_row_blocks, int32_t apply_gelu, hipStream_t stream) {
+  if (!reduction_fits<SddPairTile>(d_model) || !reduction_fits<SddNarrowTile>(d_model))
+    return fail(SB_ERR_INVALID, "sdd_experts: D (%lld) is not a whole number of the tiles' K steps",
+                static_cast<long long>(d_model));
   const int64_t grid = int64_t{kNumXcd} * pair_units_per_xcd(static_cast<int>(max_row_blocks)) * (ffn_dim / SddPairTile::BN);
   sdd_pair_kernel<SddPairTile, SddNarrowTile><<<static_cast<uint32_t>(grid), SddPairTile::kThreads, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, tokens_per_expert, padded_offsets,
@@ -575,6 +582,9 @@ int launch_dsd_layer(const void* h, const void* w2, const int32_t* tokens_per_ex
                      const int32_t* row_block_expert, void* out, int64_t max_row_blocks, int64_t num_experts,
                      int64_t num_copies, int64_t ffn_dim, int64_t d_model, int32_t force, hipStream_t stream) {
   static_assert(CfgB::BN == 512 || CfgB::BN == 256, "row-block tile widths of dsd_layer_grid");
+  if (!reduction_fits<CfgB>(ffn_dim) || !reduction_fits<DsdCfg<4, kDsdBN, WAVES, kDsdStages>>(ffn_dim))
+    return fail(SB_ERR_INVALID, "dsd_experts: F (%lld) is not a whole number of the tiles' K steps",
+                static_cast<long long>(ffn_dim));
   int64_t tiles = 0;
   if (const int rc = dsd_layer_grid(max_row_blocks, num_experts, d_model, force, &tiles)) return rc;
   const int64_t h_bytes = max_row_blocks * (ffn_dim / kBS) * kBS * kBS * 2;

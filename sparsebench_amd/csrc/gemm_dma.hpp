@@ -144,6 +144,16 @@ struct DmaCfg {
   static_assert(EPI_PARTS == 1 || (WM == 1 && TM % EPI_PARTS == 0), "epilogue parts of whole row groups");
 };
 
+// Whether a reduction of k elements runs on Cfg's main loop: whole K steps,
+// and with APAIR an even number of them (run_paired and run_paired_xs load
+// A two steps at a time and count their waits for an even count; with an
+// odd one the last pair is never loaded). Every launch of a paired tile
+// checks it on the host next to its other shape checks.
+template <class Cfg>
+constexpr bool reduction_fits(int64_t k) {
+  return k > 0 && k % Cfg::BK == 0 && (!Cfg::APAIR || (k / Cfg::BK) % 2 == 0);
+}
+
 // A rows are BK/8 16-byte chunks: logical chunk c of row r sits at c ^ swz_a(r).
 // 16 consecutive rows read at one logical chunk hit 16 different 16-byte bank
 // groups of the 256-byte bank span.
@@ -684,6 +694,7 @@ struct DmaMainloop {
     }
   }
 
+  // num_steps: with APAIR an even count (reduction_fits).
   template <class Src>
   __device__ __forceinline__ static void run(uint8_t* lds, const Src& src, int num_steps, Acc& acc) {
 #pragma unroll

@@ -470,9 +470,10 @@ extern "C" int sb_routing_assigned(const void* expert_of_copy, int32_t expert_is
 // harness that forbids hipMalloc) passes only inputs and outputs.
 //
 // The host never names `scratch` itself (its host-side symbol is not a
-// device address): on the first call on a device, with that device
-// current, hipGetSymbolAddress gives that device's copy, and the pointer is
-// kept per device and passed to the kernels.
+// device address): on the first call on a device (the device of the call's
+// stream), with that device current, hipGetSymbolAddress gives that
+// device's copy, and the pointer is kept per device and passed to the
+// kernels.
 //
 // Nothing in it has to start at zero: the count kernel writes every entry
 // of the chunks it covers before the offsets kernel reads it. Calls that
@@ -486,17 +487,32 @@ constexpr int64_t kScratchElems = int64_t{1} << 19;
 
 __device__ __attribute__((aligned(256))) int32_t scratch[kScratchElems];
 
-int scratch_on_current_device(int32_t** out) {
+// The array of the device that `stream` belongs to (the current device for
+// the null stream): the kernels run there, whichever device is current.
+int scratch_for_stream(hipStream_t stream, int32_t** out) {
   constexpr int kMaxDevices = 64;
   static std::mutex mu;
   static int32_t* ptrs[kMaxDevices] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(SB_ERR_HIP, "routing_noalloc: no current device");
+  int current = 0;
+  if (hipGetDevice(&current) != hipSuccess) return fail(SB_ERR_HIP, "routing_noalloc: no current device");
+  int dev = current;
+  if (stream != nullptr) {
+    hipDevice_t d = 0;
+    if (hipStreamGetDevice(stream, &d) != hipSuccess)
+      return fail(SB_ERR_HIP, "routing_noalloc: cannot read the stream's device");
+    dev = static_cast<int>(d);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail(SB_ERR_HIP, "routing_noalloc: device %d out of range", dev);
   std::lock_guard<std::mutex> lock(mu);
   if (ptrs[dev] == nullptr) {
+    // hipGetSymbolAddress answers for the current device: make the
+    // stream's device current for the lookup, then restore the caller's.
+    if (dev != current && hipSetDevice(dev) != hipSuccess)
+      return fail(SB_ERR_HIP, "routing_noalloc: cannot select device %d", dev);
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != current && hipSetDevice(current) != hipSuccess)
+      return fail(SB_ERR_HIP, "routing_noalloc: cannot restore device %d", current);
     if (e != hipSuccess || p == nullptr)
       return fail(SB_ERR_HIP, "routing_noalloc: hipGetSymbolAddress of the scratch array failed: %s",
                   hipGetErrorString(e));
@@ -525,7 +541,7 @@ extern "C" int sb_routing_noalloc(const void* expert_idx, int32_t idx_is_i64, in
                 static_cast<long long>(num_tokens * k), num_experts, static_cast<long long>(ws),
                 static_cast<long long>(kScratchElems));
   int32_t* ws_ptr = nullptr;
-  if (int rc = scratch_on_current_device(&ws_ptr)) return rc;
+  if (int rc = scratch_for_stream(as_stream(stream), &ws_ptr)) return rc;
   return sb_routing(expert_idx, idx_is_i64, num_tokens, k, num_experts, ffn_dim, block_size, valid_tokens, ws_ptr,
                     tokens_per_expert, padded_offsets, row_token, copy_row, row_block_expert, row_offsets,
                     col_indices, error, stream);

@@ -41,6 +41,9 @@ template <class Cfg, bool kWideX>
 int launch_sdd(const void* x, const void* w1, const int32_t* row_token, const int32_t* row_block_expert,
                const int32_t* row_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
                int64_t num_experts, int64_t num_row_blocks, int32_t apply_gelu, hipStream_t stream) {
+  if (!reduction_fits<Cfg>(d_model))
+    return fail(SB_ERR_INVALID, "sdd: D (%lld) is not a whole number of the tile's K steps",
+                static_cast<long long>(d_model));
   const int32_t num_slices = static_cast<int32_t>(ffn_dim / Cfg::BN);
   const int64_t tiles = num_row_blocks * num_slices;
   sdd_dma_kernel<Cfg, kWideX><<<static_cast<uint32_t>(tiles), Cfg::kThreads, 0, stream>>>(

@@ -140,3 +140,17 @@ def test_router_rejects_cpu_scores() -> None:
         token_rounding(torch.rand(10, 4), 2)
     with pytest.raises(RuntimeError, match="CUDA"):
         top_k_assignments(torch.rand(10, 4), 2)
+
+
+def test_reference_support_modules_are_not_provided() -> None:
+    # The import path covers the forward path only; the reference's benchmark
+    # and test support modules are absent, as INTEGRATION.md states.
+    import importlib
+
+    import sparsebench.topology
+
+    for name in ("sparsebench.reference", "sparsebench.timing", "sparsebench.baselines"):
+        with pytest.raises(ImportError):
+            importlib.import_module(name)
+    for fn in ("build_topology", "bsr_to_dense", "dense_to_bsr"):
+        assert not hasattr(sparsebench.topology, fn)

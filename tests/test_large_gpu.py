@@ -9,7 +9,8 @@ over experts). Gates: max |out - ref| / max |ref| <= 2e-2 and the
 reference's assert_close(rtol=3e-2, atol=3e-2) (tests/test_moe.py:18-34).
 
 x over 2 GiB: the reference indexes x in 64 bits (csrc/sdd.cu:71-72) and
-accepts any x (sdd.cu:151-153). At T = 264192, D = 4096 (x = 2.16 GB) the
+accepts any x (sdd.cu:151-153). At T = 264192, D = 4096 and at T = 528384,
+D = 2048 with F = 512 and 768 (x = 2.16 GB, one shape per SDD tile form) the
 SDD gathers rows past the 2 GiB mark; sampled H rows, including every row of
 the highest token ids, are checked against GELU(x[token] @ W1[e]) in fp64.
 """
@@ -46,10 +47,19 @@ def test_benchmark_shape_against_oracle(name: str, routing: str, num: int) -> No
 
 
 WIDE = LayerShape("wide_x", 264192, 4096, 512, 8)
+# x over 2 GiB in each of sb_sdd's three tile forms (sdd_tile_for): the
+# deep 128 x 512 tile (D >= 4096), the wide one (D < 4096, F % 512 == 0) and
+# the narrow 128 x 256 tile (F % 512 != 0), each gathering x with 64-bit
+# addresses.
+WIDE_FORMS = {
+    "deep": WIDE,
+    "wide": LayerShape("wide_x_d2048", 528384, 2048, 512, 8),
+    "narrow": LayerShape("wide_x_f768", 528384, 2048, 768, 8),
+}
 
 
-def wide_inputs():
-    x, idx, gates, w1, w2 = make_layer(WIDE, "random", seed=3)
+def wide_inputs(shape: LayerShape = WIDE):
+    x, idx, gates, w1, w2 = make_layer(shape, "random", seed=3)
     assert x.numel() * x.element_size() > 2**31
     return x, idx, gates, w1, w2
 
@@ -65,22 +75,24 @@ def sampled_rows(row_token: torch.Tensor, num_rows: int, num_tokens: int) -> tor
     return torch.cat([top, rnd, pad[:16]]).unique()
 
 
-@pytest.mark.parametrize("entry", ["sdd_cuda", "sdd_experts_cuda"])
-def test_sdd_accepts_x_over_2gib(entry: str) -> None:
+@pytest.mark.parametrize(("entry", "form"), [("sdd_cuda", "deep"), ("sdd_experts_cuda", "deep"),
+                                             ("sdd_experts_cuda", "wide"), ("sdd_experts_cuda", "narrow")])
+def test_sdd_accepts_x_over_2gib(entry: str, form: str) -> None:
     from sparsebench_amd import _C
     from sparsebench_amd.routing import route_device
     from sparsebench_amd.spmm import sdd
 
-    x, idx, _, w1, _ = wide_inputs()
-    e, f = WIDE.num_experts, WIDE.ffn_dim
+    shape = WIDE_FORMS[form]
+    x, idx, _, w1, _ = wide_inputs(shape)
+    e, f = shape.num_experts, shape.ffn_dim
     topo = route_device(idx, e, f, 128)
     h = sdd(x, w1, topo) if entry == "sdd_cuda" else _C.sdd_experts_cuda(x, w1, topo, True)
     torch.cuda.synchronize()
     row_token = topo.row_token.cpu()
     rbe = topo.row_block_expert.cpu()
     num_rows = int(topo.padded_offsets[-1])
-    rows = sampled_rows(row_token, num_rows, WIDE.num_tokens)
-    assert (row_token[rows] >= WIDE.num_tokens - 64).sum() >= 64  # rows past the 2 GiB mark are in the sample
+    rows = sampled_rows(row_token, num_rows, shape.num_tokens)
+    assert (row_token[rows] >= shape.num_tokens - 64).sum() >= 64  # rows past the 2 GiB mark are in the sample
     fb = f // 128
     w1_cpu = w1.double().cpu()
     for r in rows.tolist():

@@ -3,9 +3,10 @@
     python -m sparsebench_amd.build
 
 Each .hip source is compiled to an object (in parallel) and linked into one
-shared library next to this file. The read-bandwidth probe, a measurement
-tool and not part of the C ABI, is linked on its own into
-libsparsebench_probe.so. The library links libamdhip64.so.7 by
+shared library next to this file. The tool library libsparsebench_probe.so,
+not part of the C ABI, is linked on its own: the read-bandwidth probe (a
+measurement tool) and CPU shims over the kernels' tile schedules (for
+tests/test_tile_schedules.py). The library links libamdhip64.so.7 by
 soname; inside a Python process that has imported torch, that resolves to the
 HIP runtime torch already loaded, so there is one runtime per process.
 """
@@ -29,7 +30,7 @@ PROBE_LIB_NAME = "libsparsebench_probe.so"
 ARCH = "gfx950"
 
 SOURCES = ["probe.hip", "routing.hip", "sdd.hip", "dsd.hip", "combine.hip", "assigned.hip", "router.hip", "experts.hip"]
-PROBE_SOURCES = ["read_probe.hip"]
+PROBE_SOURCES = ["read_probe.hip", "schedule_shims.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

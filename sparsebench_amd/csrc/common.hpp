@@ -66,12 +66,24 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, each with its own L2
 
+// A value every lane of the wave holds alike, said so for the compiler (a
+// scalar register; v_readfirstlane). The tile schedules below are also
+// compiled for the CPU (the tool library's shims, checked by
+// tests/test_tile_schedules.py), where the value is returned as it is.
+__host__ __device__ __forceinline__ int uniform(int v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_readfirstlane(v);
+#else
+  return v;
+#endif
+}
+
 // Workgroups are handed to the XCDs round-robin by id. For ids in
 // [0, live), return a permutation of [0, live) that gives each XCD one
 // contiguous range of logical tiles, so tiles that share operands (the
 // column slices of one row block, the row blocks of one expert) run on the
 // same XCD and meet in its L2. Ids >= live map to themselves.
-__device__ __forceinline__ int xcd_remap(int bid, int live) {
+__host__ __device__ __forceinline__ int xcd_remap(int bid, int live) {
   if (bid >= live) return bid;
   const int per = live / kNumXcd;
   const int rem = live % kNumXcd;
@@ -92,7 +104,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int live) {
 struct TailTile {
   int tile, half;
 };
-__device__ __forceinline__ TailTile split_tail(int bid, int tiles, int cus_per_xcd) {
+__host__ __device__ __forceinline__ TailTile split_tail(int bid, int tiles, int cus_per_xcd) {
   const int per = tiles / kNumXcd;
   const int rem = tiles % kNumXcd;
   const int x = bid % kNumXcd;
@@ -109,13 +121,13 @@ __device__ __forceinline__ TailTile split_tail(int bid, int tiles, int cus_per_x
     t.tile = start + whole + (q - whole) / 2;
     t.half = (q - whole) % 2;
   }
-  t.tile = __builtin_amdgcn_readfirstlane(t.tile);
-  t.half = __builtin_amdgcn_readfirstlane(t.half);
+  t.tile = uniform(t.tile);
+  t.half = uniform(t.half);
   return t;
 }
 
 // Extra workgroups a grid of split_tail needs beyond its tiles.
-inline int64_t split_tail_slack(int cus) { return kNumXcd * (cus / kNumXcd / 2 + 1); }
+__host__ __device__ inline int64_t split_tail_slack(int cus) { return kNumXcd * (cus / kNumXcd / 2 + 1); }
 
 // Logical tile -> (row block, column slice) for the live region: tiles are
 // taken in groups of `group` row blocks, walking down the group one column
@@ -126,7 +138,8 @@ inline int64_t split_tail_slack(int cus) { return kNumXcd * (cus / kNumXcd / 2 +
 // integer divisions run on the vector unit, and a result left in a VGPR
 // stays live across the caller's main loop (the layer kernels, which use
 // all 512 registers, spilled it to scratch).
-__device__ __forceinline__ void tile_coords(int tile, int live_rb, int slices, int group, int* rb, int* slice) {
+__host__ __device__ __forceinline__ void tile_coords(int tile, int live_rb, int slices, int group, int* rb,
+                                                     int* slice) {
   int r, s;
   if (tile >= live_rb * slices || group <= 1) {
     r = tile / slices;
@@ -135,13 +148,13 @@ __device__ __forceinline__ void tile_coords(int tile, int live_rb, int slices, i
     const int per_group = group * slices;
     const int g = tile / per_group;
     const int first = g * group;
-    const int size = min(group, live_rb - first);
+    const int size = group < live_rb - first ? group : live_rb - first;
     const int local = tile - g * per_group;
     r = first + local % size;
     s = local / size;
   }
-  *rb = __builtin_amdgcn_readfirstlane(r);
-  *slice = __builtin_amdgcn_readfirstlane(s);
+  *rb = uniform(r);
+  *slice = uniform(s);
 }
 
 // Number of leading row blocks that can hold work. The routing layout puts

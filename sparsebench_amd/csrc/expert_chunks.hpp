@@ -267,14 +267,10 @@ __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __rest
 // expert's row blocks two by two from its first, an odd last one alone. A
 // pair is 256 padded rows (8 row groups), a single 128 (4); the tile
 // computes every padded row, so padding rows come out as zeros, as from the
-// per-row-block kernel. Units are numbered in expert order, each expert's
-// pairs before its single. For spreading them over the XCDs a pair costs
-// kPairCost and a single kSingleCost: measured tile times at D = 2048
-// (config 5), 69 and 46 us.
-constexpr int kPairCost = 10, kSingleCost = 7;
-
+// per-row-block kernel. Units are numbered in expert order, pairs and
+// singles each counted on their own.
 struct PairCounts {
-  int32_t pairs, singles, cost;
+  int32_t pairs, singles;
 };
 
 // first: expert_counts(tokens_per_expert, num_experts, 0).
@@ -291,45 +287,27 @@ __device__ __forceinline__ PairCounts pair_counts(const int32_t* __restrict__ to
   PairCounts c;
   c.pairs = wave_inclusive_scan_total(p);
   c.singles = wave_inclusive_scan_total(s);
-  c.cost = c.pairs * kPairCost + c.singles * kSingleCost;
   return c;
 }
 
-// The first unit whose cost start (the summed cost of the units before it)
-// is at least `target`, as the numbers of pairs and of singles before it
-// (all of them if there is none).
-struct UnitsBefore {
-  int32_t pairs, singles;
-};
+// The units of the pair kernel's workgroups: XCD x takes the x-th eighth of
+// the pairs and the x-th eighth of the singles, each kind in expert order,
+// and runs its pairs, then its singles, each unit's `slices` column slices
+// side by side. Workgroup bid (on XCD bid % 8) gets unit k of its kind and
+// column slice `slice`; false past the XCD's units.
+__host__ __device__ constexpr int pair_units_per_xcd(int units) { return units / kNumXcd + 2; }
 
-__device__ __forceinline__ UnitsBefore first_pair_unit_at(const int32_t* __restrict__ tokens_per_expert,
-                                                          int32_t num_experts, int target, int32_t first) {
-  int cost_before = 0, pairs_before = 0, singles_before = 0;  // over the experts before this pass
-#pragma unroll 1
-  for (int base = 0; base < num_experts; base += 64) {
-    const int32_t n = base == 0 ? first : expert_counts(tokens_per_expert, num_experts, base);
-    const int rb = n > 0 ? (n + kBS - 1) / kBS : 0;
-    const int p = rb >> 1, sg = rb & 1;
-    const int cost = p * kPairCost + sg * kSingleCost;
-    const int cincl = wave_inclusive_scan(cost);
-    const int pincl = wave_inclusive_scan(p);
-    const int sincl = wave_inclusive_scan(sg);
-    if (target < cost_before + lane_value(cincl, 63)) {
-      const int l = __builtin_ctzll(__ballot(cost_before + cincl > target));  // the expert whose costs cover target
-      const int off = target - (cost_before + lane_value(cincl - cost, l));   // 0 <= off < its cost
-      const int p_l = lane_value(p, l);
-      // Its units start at off 0, kPairCost, ..., p_l * kPairCost (the single).
-      const int i = off <= 0 ? 0 : (off <= p_l * kPairCost ? (off + kPairCost - 1) / kPairCost : p_l + 1);
-      UnitsBefore u;
-      u.pairs = pairs_before + lane_value(pincl - p, l) + min(i, p_l);
-      u.singles = singles_before + lane_value(sincl - sg, l) + (i > p_l ? 1 : 0);
-      return u;
-    }
-    cost_before += lane_value(cincl, 63);
-    pairs_before += lane_value(pincl, 63);
-    singles_before += lane_value(sincl, 63);
-  }
-  return {pairs_before, singles_before};
+__host__ __device__ __forceinline__ bool pair_unit_for(int bid, int pairs, int singles, int slices, bool* single, int* k,
+                                                       int* slice) {
+  const int q = bid / kNumXcd, x = bid % kNumXcd;
+  const int p_lo = pairs * x / kNumXcd, p_hi = pairs * (x + 1) / kNumXcd;
+  const int s_lo = singles * x / kNumXcd, s_hi = singles * (x + 1) / kNumXcd;
+  const int u = q / slices, np = p_hi - p_lo, ns = s_hi - s_lo;
+  if (u >= np + ns) return false;
+  *single = u >= np;
+  *k = uniform(u >= np ? s_lo + u - np : p_lo + u);
+  *slice = uniform(q % slices);
+  return true;
 }
 
 // Pair k (single = false) or single k (single = true), each kind counted in
@@ -376,15 +354,15 @@ __device__ __forceinline__ Chunk find_pair_unit(const int32_t* __restrict__ toke
 // that free up first are the smallest. Workgroups are handed to the XCDs
 // round-robin by id. Returns false past the XCD's tiles (the grid needs up
 // to kNumXcd x ceil(chunks / kNumXcd) x slices workgroups).
-__device__ __forceinline__ bool balanced_chunk_tile(int bid, int chunks, int slices, int* rank, int* slice) {
+__host__ __device__ __forceinline__ bool balanced_chunk_tile(int bid, int chunks, int slices, int* rank, int* slice) {
   const int x = bid % kNumXcd, q = bid / kNumXcd;
   const int rows = chunks / kNumXcd, rem = chunks % kNumXcd;
   const int pos = (rows & 1) ? kNumXcd - 1 - x : x;  // x's place in the partial row
   const int n = rows + (pos < rem ? 1 : 0);           // chunks of XCD x
   if (n == 0 || q >= n * slices) return false;
   const int j = q % n;
-  *slice = __builtin_amdgcn_readfirstlane(q / n);
-  *rank = __builtin_amdgcn_readfirstlane(kNumXcd * j + ((j & 1) ? kNumXcd - 1 - x : x));
+  *slice = uniform(q / n);
+  *rank = uniform(kNumXcd * j + ((j & 1) ? kNumXcd - 1 - x : x));
   return true;
 }
 

@@ -282,20 +282,16 @@ __global__ void __launch_bounds__(64 * kSddWaves)
 // (expert_chunks.hpp). A pair is one 256 x 256 tile of 8 waves (two rows of
 // 4, 128 x 64 each), so each W1 slice is streamed once per two row blocks
 // of an expert instead of once per row block; a single is the per-row-block
-// kernel's 128 x 256 tile. XCD x takes the units whose cost starts fall in
-// the x-th eighth of the total, so the XCDs get like shares of the work and
-// an expert's units stay on one or two XCDs, which then stream its W1 from
-// HBM once. An XCD runs its pairs, then its singles, so the tiles handed to
-// the CUs that free up last are the short ones; a unit's slices run side by
-// side (sharing its x rows), and so do an expert's pairs (sharing its W1
+// kernel's 128 x 256 tile. XCD x takes the x-th eighth of the pairs and the
+// x-th eighth of the singles, each kind in expert order: every XCD gets the
+// same mix of the two tile sizes (so no XCD's rounds are all pairs, which
+// left its singles a round of their own), and an expert's units stay on a
+// few neighbouring XCDs, which then stream its W1 from HBM once each. An XCD
+// runs its pairs, then its singles, so the tiles handed to the CUs that
+// free up last are the short ones; a unit's slices run side by side
+// (sharing its x rows), and so do an expert's pairs (sharing its W1
 // slices). Every padded row is written, so either DSD tiling may follow.
 using SddPairTile = DmaCfg<256, 256, 32, 4, 2, 4, 0, 2, 5, 1, 1>;
-
-// Units one XCD can get: at most an eighth of the cost plus one pair, all
-// singles in the worst case.
-__host__ __device__ constexpr int pair_units_per_xcd(int units) {
-  return (units * kPairCost / kNumXcd + kPairCost) / kSingleCost + 1;
-}
 
 template <class CfgP, class CfgS>
 __global__ void __launch_bounds__(CfgP::kThreads)
@@ -307,26 +303,17 @@ __global__ void __launch_bounds__(CfgP::kThreads)
   static_assert(CfgP::kThreads == CfgS::kThreads && CfgP::BN == CfgS::BN, "one workgroup and slice width");
   static_assert(CfgP::BM == 2 * kBS && CfgS::BM == kBS, "pairs and singles of row blocks");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[max_int(CfgP::kLdsAlloc, CfgS::kLdsAlloc)];
-  // Workgroup bid is XCD bid % 8's tile bid / 8 (units x slices, unit-major).
+  // Workgroup bid is XCD bid % 8's tile bid / 8 (units x slices, unit-major;
+  // pair_unit_for).
   const int32_t first = expert_counts(tokens_per_expert, num_experts, 0);
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   const int slices = ffn_dim / CfgP::BN;
-  const int q = static_cast<int>(blockIdx.x) / kNumXcd, xcd = static_cast<int>(blockIdx.x) % kNumXcd;
-  if (q >= pair_units_per_xcd(live_rb) * slices) return;
+  if (static_cast<int>(blockIdx.x) / kNumXcd >= pair_units_per_xcd(live_rb) * slices) return;
   const PairCounts pc = pair_counts(tokens_per_expert, num_experts, first);
-  const UnitsBefore lo =
-      first_pair_unit_at(tokens_per_expert, num_experts, (pc.cost * xcd + kNumXcd - 1) / kNumXcd, first);
-  const UnitsBefore hi = xcd == kNumXcd - 1
-                             ? UnitsBefore{pc.pairs, pc.singles}
-                             : first_pair_unit_at(tokens_per_expert, num_experts,
-                                                  (pc.cost * (xcd + 1) + kNumXcd - 1) / kNumXcd, first);
-  // The XCD's pairs, then its singles (largest first), each unit's slices side by side.
-  const int u = q / slices, slice = q % slices;
-  const int np = hi.pairs - lo.pairs, ns = hi.singles - lo.singles;
-  if (u >= np + ns) return;
-  const bool single = u >= np;
-  const Chunk ch = find_pair_unit(tokens_per_expert, num_experts, single, single ? lo.singles + u - np : lo.pairs + u,
-                                  first);
+  bool single;
+  int k, slice;
+  if (!pair_unit_for(static_cast<int>(blockIdx.x), pc.pairs, pc.singles, slices, &single, &k, &slice)) return;
+  const Chunk ch = find_pair_unit(tokens_per_expert, num_experts, single, k, first);
   // Not a routing layout (the unit would leave the buffers): skip it.
   if (ch.expert < 0 || ch.expert >= num_experts || ch.row0 < 0 || ch.rows < 1 ||
       ch.row0 + 32 * ch.groups > max_row_blocks * kBS)

@@ -1,77 +1,73 @@
-"""The layer kernels' tile schedules, restated on the CPU: every tile of a
-stage is handed to exactly one workgroup of the grid the host launches.
+"""The layer kernels' tile schedules on the CPU: every tile of a stage is
+handed to exactly one workgroup of the grid the host launches.
 
 A workgroup that finds no tile returns, so a grid bound that is too small,
 or a mapping that hands one tile to two workgroups, would leave output rows
 unwritten or written twice without any error on the GPU. These tests walk
-every workgroup id of the launched grid through the mappings of
-csrc/common.hpp (split_tail, split_tail_slack), csrc/expert_chunks.hpp
-(balanced_chunk_tile, pair_counts, first_pair_unit_at, find_pair_unit) and
-csrc/experts.hip (sdd_pair_kernel, pair_units_per_xcd) over many layouts.
+every workgroup id of the launched grid through the mappings the kernels
+call: csrc/common.hpp (xcd_remap, split_tail, split_tail_slack, tile_coords)
+and csrc/expert_chunks.hpp (balanced_chunk_tile, pair_units_per_xcd,
+pair_unit_for) are __host__ __device__ functions, compiled for the CPU into
+the tool library's shims (csrc/schedule_shims.hip), so what is checked here
+is the compiled code, not a restatement of it. What each workgroup must
+cover is stated independently below (the live row blocks, each kind of pair
+unit in expert order).
 """
 from __future__ import annotations
+
+import ctypes
 
 import numpy as np
 import pytest
 
+from sparsebench_amd import _lib
+
 XCD = 8
 BS = 128
-PAIR_COST, SINGLE_COST = 10, 7
 
 
-def split_tail(bid: int, tiles: int, cus_per_xcd: int) -> tuple[int, int]:
-    per, rem = divmod(tiles, XCD)
-    x, q = bid % XCD, bid // XCD
-    n = per + (1 if x < rem else 0)
-    start = x * (per + 1) if x < rem else rem * (per + 1) + (x - rem) * per
-    r = n % cus_per_xcd if cus_per_xcd > 0 else 0
-    split = r if (r > 0 and 2 * r <= cus_per_xcd) else 0
-    whole = n - split
-    if q < whole:
-        return start + q, -1
-    if q < whole + 2 * split:
-        return start + whole + (q - whole) // 2, (q - whole) % 2
-    return tiles, -1
+@pytest.fixture(scope="module")
+def sched():
+    path = _lib.LIB_PATH.with_name("libsparsebench_probe.so")
+    if not path.exists():
+        from sparsebench_amd.build import build
+
+        build()
+    _lib.lib()  # torch's HIP runtime first
+    h = ctypes.CDLL(str(path))
+    ip = ctypes.POINTER(ctypes.c_int)
+    i = ctypes.c_int
+    for name, res, args in [
+        ("sbt_xcd_remap", i, [i, i]),
+        ("sbt_split_tail", None, [i, i, i, ip, ip]),
+        ("sbt_split_tail_slack", ctypes.c_int64, [i]),
+        ("sbt_tile_coords", None, [i, i, i, i, ip, ip]),
+        ("sbt_balanced_chunk_tile", i, [i, i, i, ip, ip]),
+        ("sbt_pair_units_per_xcd", i, [i]),
+        ("sbt_pair_unit_for", i, [i, i, i, i, ip, ip, ip]),
+    ]:
+        fn = getattr(h, name)
+        fn.restype = res
+        fn.argtypes = args
+    return h
 
 
-def split_tail_slack(cus: int) -> int:
-    return XCD * (cus // XCD // 2 + 1)
+def split_tail(sched, bid: int, tiles: int, cus_per_xcd: int) -> tuple[int, int]:
+    t, hf = ctypes.c_int(), ctypes.c_int()
+    sched.sbt_split_tail(bid, tiles, cus_per_xcd, ctypes.byref(t), ctypes.byref(hf))
+    return t.value, hf.value
 
 
-def balanced_chunk_tile(bid: int, chunks: int, slices: int):
-    x, q = bid % XCD, bid // XCD
-    rows, rem = divmod(chunks, XCD)
-    pos = XCD - 1 - x if rows & 1 else x
-    n = rows + (1 if pos < rem else 0)
-    if n == 0 or q >= n * slices:
+def balanced_chunk_tile(sched, bid: int, chunks: int, slices: int):
+    r, s = ctypes.c_int(), ctypes.c_int()
+    if not sched.sbt_balanced_chunk_tile(bid, chunks, slices, ctypes.byref(r), ctypes.byref(s)):
         return None
-    j = q % n
-    return XCD * j + (XCD - 1 - x if j & 1 else x), q // n
-
-
-def pair_units_per_xcd(units: int) -> int:
-    return (units * PAIR_COST // XCD + PAIR_COST) // SINGLE_COST + 1
-
-
-def first_pair_unit_at(counts: list[int], target: int) -> tuple[int, int]:
-    """(pairs, singles) before the first unit whose cost start is >= target."""
-    cost_before = pairs_before = singles_before = 0
-    for n in counts:
-        rb = -(-n // BS) if n > 0 else 0
-        p, s = rb >> 1, rb & 1
-        cost = p * PAIR_COST + s * SINGLE_COST
-        if target < cost_before + cost:
-            off = target - cost_before
-            i = 0 if off <= 0 else (-(-off // PAIR_COST) if off <= p * PAIR_COST else p + 1)
-            return pairs_before + min(i, p), singles_before + (1 if i > p else 0)
-        cost_before += cost
-        pairs_before += p
-        singles_before += s
-    return pairs_before, singles_before
+    return r.value, s.value
 
 
 def pair_unit_rows(counts: list[int], single: bool, k: int) -> tuple[int, int]:
-    """Padded rows [row0, row0 + 128 * blocks) of pair k or single k (each kind in expert order)."""
+    """Padded rows [row0, row0 + 128 * blocks) of pair k or single k (each
+    kind in expert order): the units find_pair_unit numbers."""
     off = 0
     for n in counts:
         rb = -(-n // BS) if n > 0 else 0
@@ -84,27 +80,22 @@ def pair_unit_rows(counts: list[int], single: bool, k: int) -> tuple[int, int]:
     raise AssertionError("unit past the layout")
 
 
-def pair_kernel_tiles(counts: list[int], max_row_blocks: int, slices: int) -> list[tuple[int, int]]:
-    """(first padded row, slice) of every tile sdd_pair_kernel computes, over its whole grid."""
+def pair_kernel_tiles(sched, counts: list[int], max_row_blocks: int, slices: int) -> list[tuple[int, int]]:
+    """(row block, slice) of every tile sdd_pair_kernel computes, over its whole grid."""
     live_rb = sum(-(-n // BS) for n in counts if n > 0)
     pairs = sum((-(-n // BS) >> 1) for n in counts if n > 0)
     singles = sum((-(-n // BS) & 1) for n in counts if n > 0)
-    cost = pairs * PAIR_COST + singles * SINGLE_COST
-    grid = XCD * pair_units_per_xcd(max_row_blocks) * slices
+    grid = XCD * sched.sbt_pair_units_per_xcd(max_row_blocks) * slices
+    single, k, sl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     tiles = []
     for bid in range(grid):
-        q, x = divmod(bid, XCD)
-        if q >= pair_units_per_xcd(live_rb) * slices:
+        if bid // XCD >= sched.sbt_pair_units_per_xcd(live_rb) * slices:
+            continue  # the kernel's first exit test
+        if not sched.sbt_pair_unit_for(bid, pairs, singles, slices, ctypes.byref(single), ctypes.byref(k),
+                                       ctypes.byref(sl)):
             continue
-        lo = first_pair_unit_at(counts, (cost * x + XCD - 1) // XCD)
-        hi = (pairs, singles) if x == XCD - 1 else first_pair_unit_at(counts, (cost * (x + 1) + XCD - 1) // XCD)
-        u, sl = divmod(q, slices)
-        np_, ns = hi[0] - lo[0], hi[1] - lo[1]
-        if u >= np_ + ns:
-            continue
-        single = u >= np_
-        row0, nrows = pair_unit_rows(counts, single, lo[1] + u - np_ if single else lo[0] + u)
-        tiles.extend((r, sl) for r in range(row0 // BS, (row0 + nrows) // BS))
+        row0, nrows = pair_unit_rows(counts, bool(single.value), k.value)
+        tiles.extend((r, sl.value) for r in range(row0 // BS, (row0 + nrows) // BS))
     return tiles
 
 
@@ -125,44 +116,66 @@ def layouts():
 
 
 @pytest.mark.parametrize("slices", [1, 3, 8])
-def test_pair_kernel_covers_every_live_row_block_once(slices: int) -> None:
+def test_pair_kernel_covers_every_live_row_block_once(sched, slices: int) -> None:
     for counts in layouts():
         copies = sum(counts)
         e = len(counts)
         max_rb = (copies + e * (BS - 1)) // BS  # the routing's worst-case sizing
-        tiles = pair_kernel_tiles(counts, max_rb, slices)
+        tiles = pair_kernel_tiles(sched, counts, max_rb, slices)
         live_rb = sum(-(-n // BS) for n in counts if n > 0)
         assert sorted(tiles) == [(r, s) for r in range(live_rb) for s in range(slices)], counts
 
 
-def test_pair_units_per_xcd_bounds_each_xcds_range() -> None:
-    for counts in layouts():
-        live_rb = sum(-(-n // BS) for n in counts if n > 0)
-        pairs = sum((-(-n // BS) >> 1) for n in counts if n > 0)
-        singles = sum((-(-n // BS) & 1) for n in counts if n > 0)
-        cost = pairs * PAIR_COST + singles * SINGLE_COST
-        ranges = [first_pair_unit_at(counts, (cost * x + XCD - 1) // XCD) for x in range(XCD)] + [(pairs, singles)]
-        for x in range(XCD):
-            n = (ranges[x + 1][0] - ranges[x][0]) + (ranges[x + 1][1] - ranges[x][1])
-            assert 0 <= n <= pair_units_per_xcd(live_rb), (counts, x)
+def test_pair_kernel_xcds_share_each_kind_evenly(sched) -> None:
+    # Each XCD's pairs and singles are within one unit of an eighth of each kind.
+    single, k, sl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    for pairs, singles in [(114, 101), (0, 7), (5, 0), (31, 1), (1000, 3)]:
+        per = [[0, 0] for _ in range(XCD)]
+        for bid in range(XCD * sched.sbt_pair_units_per_xcd(pairs + singles)):
+            if sched.sbt_pair_unit_for(bid, pairs, singles, 1, ctypes.byref(single), ctypes.byref(k), ctypes.byref(sl)):
+                per[bid % XCD][single.value] += 1
+        assert sum(p for p, _ in per) == pairs and sum(s for _, s in per) == singles
+        assert max(p for p, _ in per) - min(p for p, _ in per) <= 1
+        assert max(s for _, s in per) - min(s for _, s in per) <= 1
 
 
 @pytest.mark.parametrize("slices", [1, 2, 8, 28])
-def test_balanced_deal_hands_out_every_chunk_slice_once(slices: int) -> None:
+def test_balanced_deal_hands_out_every_chunk_slice_once(sched, slices: int) -> None:
     for chunks in list(range(0, 70)) + [130, 255, 256, 257, 1000]:
         grid = XCD * (-(-chunks // XCD)) * slices  # the kernels' grids hold at least this many
-        seen = [balanced_chunk_tile(b, chunks, slices) for b in range(grid + 3 * XCD)]
+        seen = [balanced_chunk_tile(sched, b, chunks, slices) for b in range(grid + 3 * XCD)]
         got = sorted(t for t in seen if t is not None)
         assert got == [(c, s) for c in range(chunks) for s in range(slices)], chunks
 
 
 @pytest.mark.parametrize("cus", [256, 304, 80])
-def test_split_tail_covers_every_tile_once(cus: int) -> None:
+def test_split_tail_covers_every_tile_once(sched, cus: int) -> None:
     for tiles in list(range(0, 200)) + [511, 512, 513, 848, 987, 1316, 1932]:
         halves: dict[int, list[int]] = {}
-        for b in range(tiles + split_tail_slack(cus)):
-            t, h = split_tail(b, tiles, cus // XCD)
+        for b in range(tiles + sched.sbt_split_tail_slack(cus)):
+            t, h = split_tail(sched, b, tiles, cus // XCD)
             if t < tiles:
                 halves.setdefault(t, []).append(h)
         assert sorted(halves) == list(range(tiles)), tiles
         assert all(v == [-1] or sorted(v) == [0, 1] for v in halves.values()), tiles
+
+
+def test_xcd_remap_is_a_permutation_of_the_live_tiles(sched) -> None:
+    for live in list(range(0, 100)) + [256, 511, 512, 1316]:
+        got = sorted(sched.sbt_xcd_remap(b, live) for b in range(live))
+        assert got == list(range(live)), live
+        # each XCD (bid % 8) gets one contiguous range
+        for x in range(XCD):
+            mine = sorted(sched.sbt_xcd_remap(b, live) for b in range(x, live, XCD))
+            assert mine == list(range(mine[0], mine[0] + len(mine))) if mine else True
+
+
+def test_tile_coords_cover_the_live_grid_once(sched) -> None:
+    rb, sl = ctypes.c_int(), ctypes.c_int()
+    for live_rb in (1, 5, 8, 13, 64, 92):
+        for slices in (1, 2, 4, 8):
+            got = set()
+            for t in range(live_rb * slices):
+                sched.sbt_tile_coords(t, live_rb, slices, 8, ctypes.byref(rb), ctypes.byref(sl))
+                got.add((rb.value, sl.value))
+            assert got == {(r, s) for r in range(live_rb) for s in range(slices)}, (live_rb, slices)

@@ -185,7 +185,8 @@ __device__ __forceinline__ uint32_t big_chunks_of_group(const int32_t* __restric
 // Local tile `local` of a group of G chunks x `slices` slices, largest
 // first: the chunks of `big` (a mask over the group's positions) with all
 // their slices, then the rest slice by slice.
-__device__ __forceinline__ void lpt_group_tile(int local, int G, int slices, uint32_t big, int* pos, int* slice) {
+__host__ __device__ __forceinline__ void lpt_group_tile(int local, int G, int slices, uint32_t big, int* pos,
+                                                        int* slice) {
   const int nb = __builtin_popcount(big);
   uint32_t set = big;
   int idx;

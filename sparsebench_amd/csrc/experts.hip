@@ -445,7 +445,24 @@ __global__ void __launch_bounds__(64 * WAVES)
   const int slices = d_model / kDsdBN;
   const int tile = xcd_remap(static_cast<int>(blockIdx.x), chunks * slices);
   int c, slice;
-  tile_coords(tile, chunks, slices, group, &c, &slice);
+  if (chunks == sum.active || chunks > 32 * kNumXcd) {
+    tile_coords(tile, chunks, slices, group, &c, &slice);
+  } else {
+    // Experts of several chunks: groups of ceil(chunks / 8) chunks x all
+    // slices, about one XCD's share each, largest chunks first inside each
+    // group (lpt_group_tile: an expert's merged last chunk of up to 320
+    // rows, about 1.25 times a 256-row tile's time, runs in the first round,
+    // so no CU runs two of them one after the other).
+    if (tile >= chunks * slices) return;
+    const int per = (chunks + kNumXcd - 1) / kNumXcd;
+    const int g0 = (tile / (per * slices)) * per;
+    const int G = min(per, chunks - g0);
+    const uint32_t big = big_chunks_of_group<kRmax>(tokens_per_expert, num_experts, g0, G, first);
+    int pos;
+    lpt_group_tile(tile - g0 * slices, G, slices, big, &pos, &slice);
+    c = __builtin_amdgcn_readfirstlane(g0 + pos);
+    slice = __builtin_amdgcn_readfirstlane(slice);
+  }
   if (c >= chunks) return;
   const Chunk ch = find_chunk<kRmax>(tokens_per_expert, num_experts, c, first);
   if (ch.expert < 0 || ch.row0 < 0 || ch.groups < 1 || ch.groups > kRmax ||

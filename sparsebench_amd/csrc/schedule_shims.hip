@@ -1,7 +1,7 @@
 // The layer kernels' tile schedules, compiled for the CPU: extern "C" shims
 // over the same __host__ __device__ functions the kernels call
 // (common.hpp: xcd_remap, split_tail, split_tail_slack, tile_coords;
-// expert_chunks.hpp: balanced_chunk_tile, pair_units_per_xcd,
+// expert_chunks.hpp: balanced_chunk_tile, lpt_group_tile, pair_units_per_xcd,
 // pair_unit_for), so tests/test_tile_schedules.py checks the compiled
 // mappings themselves. Part of the tool library (libsparsebench_probe.so),
 // not of libsparsebench_hip.so's C ABI. No kernel runs.
@@ -35,4 +35,8 @@ extern "C" int sbt_pair_unit_for(int bid, int pairs, int singles, int slices, in
   const bool ok = pair_unit_for(bid, pairs, singles, slices, &s, k, slice);
   *single = s ? 1 : 0;
   return ok ? 1 : 0;
+}
+
+extern "C" void sbt_lpt_group_tile(int local, int groups, int slices, uint32_t big, int* pos, int* slice) {
+  lpt_group_tile(local, groups, slices, big, pos, slice);
 }

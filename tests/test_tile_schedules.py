@@ -6,8 +6,8 @@ or a mapping that hands one tile to two workgroups, would leave output rows
 unwritten or written twice without any error on the GPU. These tests walk
 every workgroup id of the launched grid through the mappings the kernels
 call: csrc/common.hpp (xcd_remap, split_tail, split_tail_slack, tile_coords)
-and csrc/expert_chunks.hpp (balanced_chunk_tile, pair_units_per_xcd,
-pair_unit_for) are __host__ __device__ functions, compiled for the CPU into
+and csrc/expert_chunks.hpp (balanced_chunk_tile, lpt_group_tile,
+pair_units_per_xcd, pair_unit_for) are __host__ __device__ functions, compiled for the CPU into
 the tool library's shims (csrc/schedule_shims.hip), so what is checked here
 is the compiled code, not a restatement of it. What each workgroup must
 cover is stated independently below (the live row blocks, each kind of pair
@@ -45,6 +45,7 @@ def sched():
         ("sbt_balanced_chunk_tile", i, [i, i, i, ip, ip]),
         ("sbt_pair_units_per_xcd", i, [i]),
         ("sbt_pair_unit_for", i, [i, i, i, i, ip, ip, ip]),
+        ("sbt_lpt_group_tile", None, [i, i, i, ctypes.c_uint32, ip, ip]),
     ]:
         fn = getattr(h, name)
         fn.restype = res
@@ -179,3 +180,20 @@ def test_tile_coords_cover_the_live_grid_once(sched) -> None:
                 sched.sbt_tile_coords(t, live_rb, slices, 8, ctypes.byref(rb), ctypes.byref(sl))
                 got.add((rb.value, sl.value))
             assert got == {(r, s) for r in range(live_rb) for s in range(slices)}, (live_rb, slices)
+
+
+def test_lpt_group_tile_runs_big_chunks_first_and_covers_the_group_once(sched) -> None:
+    # Each group of G chunks x slices is handed out once, the chunks of `big`
+    # (all their slices) before the others.
+    pos, sl = ctypes.c_int(), ctypes.c_int()
+    rng = np.random.default_rng(3)
+    for g in (1, 2, 4, 5, 8, 13, 32):
+        for slices in (1, 3, 16, 28):
+            for big in {0, (1 << g) - 1 if g < 32 else 0xFFFFFFFF, int(rng.integers(0, 1 << min(g, 31)))}:
+                order = []
+                for local in range(g * slices):
+                    sched.sbt_lpt_group_tile(local, g, slices, big, ctypes.byref(pos), ctypes.byref(sl))
+                    order.append((pos.value, sl.value))
+                assert sorted(order) == [(p, s) for p in range(g) for s in range(slices)], (g, slices, big)
+                nb = bin(big & ((1 << g) - 1)).count("1")
+                assert all((big >> p) & 1 for p, _ in order[:nb * slices]), (g, slices, big)

@@ -182,8 +182,16 @@ template <int WAVES>
 constexpr int dsd_rmax() { return WAVES == 8 ? 10 : 8; }
 
 // Expert tiles of the SDD: 8 waves, 512 columns, chunks of up to 192 rows;
-// tiles of up to 128 rows have a 4-stage ring (4 x 40 KB fits the 160 KB).
+// tiles of up to 128 rows have a 4-stage ring (4 x 40 KB fits the 160 KB),
+// 160-row tiles a split one (2 A slots of 16 KB, 4 B stages of 32 KB), and
+// 192-row tiles a 3-stage ring.
 constexpr int kSddBN = 512, kSddWaves = 8, kSddRmax = 6, kSddStages = 3;
+template <int R>
+using SddChunkCfg = std::conditional_t<
+    (R <= 4), ChunkCfg<R, kSddBN, kSddWaves, 4>,
+    std::conditional_t<(R == 5), DmaCfg<160, kSddBN, 32, 2, 1, kSddWaves, 0, 2, 5, 1, 0, 4>,
+                       ChunkCfg<R, kSddBN, kSddWaves, kSddStages>>>;
+static_assert(SddChunkCfg<5>::kLdsAlloc <= 160 * 1024, "LDS");
 
 template <class CfgB>
 __global__ void __launch_bounds__(64 * kSddWaves)
@@ -274,7 +282,7 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     return;
   with_groups<kSddRmax>(ch.groups, [&](auto rc) {
     constexpr int R = decltype(rc)::value;
-    sdd_chunk_tile<ChunkCfg<R, kSddBN, kSddWaves, (R <= 4 ? 4 : kSddStages)>>(lds, a, ch, n0_slice * kSddBN);
+    sdd_chunk_tile<SddChunkCfg<R>>(lds, a, ch, n0_slice * kSddBN);
   });
 }
 

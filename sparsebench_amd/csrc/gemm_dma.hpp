@@ -88,10 +88,17 @@ __device__ __forceinline__ void wait_vmcnt() {
 // a 64-byte row piece costs the address and data units a whole cache line,
 // so pairing halves the A lines per byte. A pair m (K steps 2m, 2m+1) sits
 // in A slot m % 2, B of step t in ring slot t % STAGES (STAGES 3 or 4).
+// BSTAGES (0: as STAGES): a B ring deeper than the A ring (PIPE 5,
+// unpaired): A of step t in slot t % STAGES, loaded STAGES-1 steps ahead,
+// B in slot t % BSTAGES, loaded BSTAGES-1 steps ahead (DmaMainloop::
+// run_split_xs). For tall tiles whose A area leaves no room for a fourth
+// whole stage: the weight stream, whose misses go to HBM, keeps its lead.
 template <int BM_, int BN_, int BK_, int STAGES_, int WM_ = 2, int WN_ = 2, int CPA_ = 0, int CPB_ = 0, int PIPE_ = 0,
-          int EPI_PARTS_ = 1, int APAIR_ = 0>
+          int EPI_PARTS_ = 1, int APAIR_ = 0, int BSTAGES_ = 0>
 struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_;
+  static constexpr int BSTAGES = BSTAGES_ > 0 ? BSTAGES_ : STAGES_;
+  static constexpr bool SPLIT = BSTAGES != STAGES;
   static constexpr int CPA = CPA_, CPB = CPB_;
   static constexpr int PIPE = PIPE_;
   static constexpr int EPI_PARTS = EPI_PARTS_;
@@ -113,7 +120,8 @@ struct DmaCfg {
   static constexpr int kBRowBytes = BN * 2;
   static constexpr int kBBytes = BK * kBRowBytes;
   static constexpr int kStageBytes = kABytes + kBBytes;
-  static constexpr int kLdsBytes = APAIR ? 2 * kABytes + STAGES * kBBytes : STAGES * kStageBytes;
+  static constexpr int kLdsBytes =
+      APAIR ? 2 * kABytes + STAGES * kBBytes : (SPLIT ? STAGES * kABytes + BSTAGES * kBBytes : STAGES * kStageBytes);
   // LDS of a kernel: the ring, or the part of the bf16 output tile staged
   // through it in the epilogue if that is larger.
   static constexpr int kStagedPartBytes = BM * BN * 2 / EPI_PARTS;
@@ -142,6 +150,11 @@ struct DmaCfg {
   static_assert(!APAIR || (BK == 32 && (STAGES == 3 || STAGES == 4) && (PIPE == 3 || PIPE == 4 || PIPE == 5)),
                 "paired A: BK 32, a 3- or 4-stage B ring, DMA among the MFMAs");
   static_assert(EPI_PARTS == 1 || (WM == 1 && TM % EPI_PARTS == 0), "epilogue parts of whole row groups");
+  static_assert(!SPLIT || (!APAIR && PIPE == 5 && BSTAGES > STAGES && STAGES >= 2 && BSTAGES <= 8),
+                "a deeper B ring: unpaired PIPE 5");
+  // The split ring's wait: loads issued after step t's A, in steady state.
+  static constexpr int kSplitLater = kBInstr + (STAGES - 2) * (kAInstr + kBInstr);
+  static_assert(!SPLIT || kSplitLater + kBInstr <= 63, "vmcnt");
 };
 
 // Whether a reduction of k elements runs on Cfg's main loop: whole K steps,
@@ -266,10 +279,12 @@ struct DmaMainloop {
   // Slots of K step t: its A (shared by a stage pair with APAIR) and its B.
   __device__ __forceinline__ static uint8_t* a_slot(uint8_t* lds, int t) {
     if constexpr (Cfg::APAIR) return lds + ((t >> 1) & 1) * Cfg::kABytes;
+    else if constexpr (Cfg::SPLIT) return lds + (t % Cfg::STAGES) * Cfg::kABytes;
     else return lds + (t % Cfg::STAGES) * Cfg::kStageBytes;
   }
   __device__ __forceinline__ static uint8_t* b_slot(uint8_t* lds, int t) {
     if constexpr (Cfg::APAIR) return lds + 2 * Cfg::kABytes + (t % Cfg::STAGES) * Cfg::kBBytes;
+    else if constexpr (Cfg::SPLIT) return lds + Cfg::STAGES * Cfg::kABytes + (t % Cfg::BSTAGES) * Cfg::kBBytes;
     else return lds + (t % Cfg::STAGES) * Cfg::kStageBytes + Cfg::kABytes;
   }
 
@@ -622,6 +637,67 @@ struct DmaMainloop {
     compute_xs<false>(a_slot(lds, t), b_slot(lds, t), t & 1, acc, NoDma{}, fr, a, b, nullptr, nullptr, 0, NoWait{});
   }
 
+  // s_waitcnt vmcnt(n) for a run-time n in [0, MAX].
+  template <int MAX>
+  __device__ __forceinline__ static void wait_vmcnt_upto(int n) {
+    static_for<0, MAX + 1>([&](auto c) {
+      if (n == decltype(c)::value) wait_vmcnt<decltype(c)::value>();
+    });
+  }
+
+  // PIPE 5 with the deeper B ring (SPLIT). Step u issues A of step
+  // u+STAGES-1, then B of step u+BSTAGES-1, each if it exists; the prologue
+  // is steps -(BSTAGES-1) .. -1 of the same rule. Loads complete in issue
+  // order and A of a step is issued after its B, so step t's data is in
+  // once at most the loads issued after its A are outstanding: that step's
+  // B (of step t+BSTAGES-STAGES) and the A and B of the STAGES-2 steps
+  // after it, those that exist (split_later).
+  __device__ __forceinline__ static int split_later(int t, int n) {
+    constexpr int SA = Cfg::STAGES, SB = Cfg::BSTAGES;
+    int later = t + SB - SA < n ? Cfg::kBInstr : 0;
+#pragma unroll
+    for (int d = 2 - SA; d <= -1; ++d) {
+      later += t + d + SA - 1 < n ? Cfg::kAInstr : 0;
+      later += t + d + SB - 1 < n ? Cfg::kBInstr : 0;
+    }
+    return later;
+  }
+
+  template <class Src>
+  __device__ __forceinline__ static void run_split_xs(uint8_t* lds, const Src& src, int n, Acc& acc) {
+    constexpr int SA = Cfg::STAGES, SB = Cfg::BSTAGES;
+    const Frags fr;
+    FragA a;
+    FragB b;
+    auto a_load = [&](int u) { return StepDma<Src, true, false>(a_slot(lds, u), u, nullptr, 0, src); };
+#pragma unroll
+    for (int u = -(SB - 1); u < 0; ++u) {
+      if (u + SA - 1 >= 0 && u + SA - 1 < n) issue_all(a_load(u + SA - 1));
+      if (u + SB - 1 < n) issue_all(b_dma(lds, u + SB - 1, src));
+    }
+    wait_vmcnt_upto<Cfg::kSplitLater>(split_later(0, n));
+    __builtin_amdgcn_s_barrier();
+    fr.read_a(a_slot(lds, 0), 0, 0, a[0]);
+    fr.read_b(b_slot(lds, 0), 0, b[0]);
+    int t = 0;
+    // Both loads of each step exist.
+    for (; t + SB - 1 < n && t + 1 < n; ++t)
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), 0, acc,
+                       StepDma<Src, true, true>(a_slot(lds, t + SA - 1), t + SA - 1, b_slot(lds, t + SB - 1),
+                                                t + SB - 1, src),
+                       fr, a, b, a_slot(lds, t + 1), b_slot(lds, t + 1), 0,
+                       [&] { wait_vmcnt_upto<Cfg::kSplitLater>(split_later(t + 1, n)); });
+    // Only A loads left.
+    for (; t + SA - 1 < n && t + 1 < n; ++t)
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), 0, acc, a_load(t + SA - 1), fr, a, b, a_slot(lds, t + 1),
+                       b_slot(lds, t + 1), 0, [&] { wait_vmcnt_upto<Cfg::kSplitLater>(split_later(t + 1, n)); });
+    // Nothing left to load.
+    for (; t + 1 < n; ++t)
+      compute_xs<true>(a_slot(lds, t), b_slot(lds, t), 0, acc, NoDma{}, fr, a, b, a_slot(lds, t + 1),
+                       b_slot(lds, t + 1), 0, [&] { wait_vmcnt_upto<Cfg::kSplitLater>(split_later(t + 1, n)); });
+    compute_xs<false>(a_slot(lds, t), b_slot(lds, t), 0, acc, NoDma{}, fr, a, b, nullptr, nullptr, 0, NoWait{});
+  }
+
   // PIPE 5, unpaired.
   template <class Src>
   __device__ __forceinline__ static void run_xs(uint8_t* lds, const Src& src, int n, Acc& acc) {
@@ -706,6 +782,7 @@ struct DmaMainloop {
     if (num_steps <= 0) return;
     if constexpr (Cfg::PIPE == 5) {
       if constexpr (Cfg::APAIR) run_paired_xs(lds, src, num_steps, acc);
+      else if constexpr (Cfg::SPLIT) run_split_xs(lds, src, num_steps, acc);
       else run_xs(lds, src, num_steps, acc);
       return;
     }

@@ -114,6 +114,16 @@ def test_combine_rejects_gate_dtype(lib) -> None:
     assert "gate dtype" in _err(lib)
 
 
+def test_combines_reject_more_than_2_31_lanes(lib) -> None:
+    # One lane per 16 bytes of output: T * D / 8 must stay below 2^31 - 255.
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
+    assert lib.sb_combine(p, p, p, 0, p, 1 << 28, 2, 64, 4, None, None) == 1
+    assert "too many tokens" in _err(lib)
+    assert lib.sb_combine_assigned(p, p, p, 0, p, None, p, 1 << 28, 64, 4, None, None) == 1
+    assert "too many tokens" in _err(lib)
+
+
 @pytest.mark.parametrize(("num_tokens", "num_experts", "k", "tile"),
                          [(4096, 64, 2, 128), (50, 3, 1, 4), (16384, 128, 2, 128), (1000, 65, 3, 16)])
 def test_router_sizes(lib, num_tokens: int, num_experts: int, k: int, tile: int) -> None:

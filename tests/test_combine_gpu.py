@@ -103,3 +103,22 @@ def test_bit_exact_to_reference_arithmetic(gate_dtype, k) -> None:
     y, copy_row, w = make(1000, k, 512, 1000 * k + 9, gate_dtype, seed=4, skipped=0.1)
     out = combine(y.cuda(), copy_row.cuda(), w.cuda()).cpu()
     assert torch.equal(out, combine_reference(y, copy_row.numpy(), w).bfloat16())
+
+
+@pytest.mark.parametrize(("num_tokens", "d_model"), [(5000, 24), (701, 1000), (333, 1032), (90, 2040), (70001, 8)])
+def test_any_row_width_bit_exact(num_tokens, d_model) -> None:
+    # Row widths of 3, 125, 129, 255 and 1 16-byte chunks: the kernels split
+    # the flat lane number into token and chunk by a multiply and a shift,
+    # which must give every lane its own (token, chunk) at any width.
+    from sparsebench_amd import _C
+    from sparsebench_amd.moe import combine
+
+    y, copy_row, w = make(num_tokens, 2, d_model, num_tokens * 2 + 3, torch.float32, seed=d_model, skipped=0.05)
+    want = combine_reference(y, copy_row.numpy(), w).bfloat16()
+    out = combine(y.cuda(), copy_row.cuda(), w.cuda()).cpu()
+    assert torch.equal(out, want)
+    # The assigned combine, with each token's copies listed in slot order.
+    offsets = torch.arange(0, 2 * num_tokens + 1, 2, dtype=torch.int32)
+    out_a = _C.combine_assigned_cuda(y.cuda(), copy_row.cuda(), w.reshape(-1).cuda(), offsets.cuda(), None,
+                                     num_tokens).cpu()
+    assert torch.equal(out_a, want)

@@ -294,20 +294,45 @@ __device__ __forceinline__ PairCounts pair_counts(const int32_t* __restrict__ to
 // The units of the pair kernel's workgroups: XCD x takes the x-th eighth of
 // the pairs and the x-th eighth of the singles, each kind in expert order,
 // and runs its pairs, then its singles, each unit's `slices` column slices
-// side by side. Workgroup bid (on XCD bid % 8) gets unit k of its kind and
-// column slice `slice`; false past the XCD's units.
+// side by side (pair_tile_for). An XCD holds at most this many units.
 __host__ __device__ constexpr int pair_units_per_xcd(int units) { return units / kNumXcd + 2; }
 
-__host__ __device__ __forceinline__ bool pair_unit_for(int bid, int pairs, int singles, int slices, bool* single, int* k,
-                                                       int* slice) {
+// Workgroup bid (on XCD bid % 8) and its tile, with a short last round
+// split. An XCD that runs n tiles on
+// `cus` CUs has r = n % cus of them in its last round; when those are all
+// singles, each runs as two column halves on workgroups of their own, so 2r
+// CUs share the round (as split_tail does for row-block tiles), if 2r CUs
+// are free when the round starts: pair tiles in the round before it (about
+// 1.6 times a single's time) still hold their CUs then, and halves past the
+// free CUs would wait for a round of their own. Workgroup bid gets unit k of
+// its kind, column slice `slice` and `half`: -1 for the whole slice, else 0
+// or 1; false past the XCD's tiles. An XCD uses positions up to n + cus / 2.
+__host__ __device__ __forceinline__ bool pair_tile_for(int bid, int pairs, int singles, int slices, int cus,
+                                                       bool* single, int* k, int* slice, int* half) {
   const int q = bid / kNumXcd, x = bid % kNumXcd;
   const int p_lo = pairs * x / kNumXcd, p_hi = pairs * (x + 1) / kNumXcd;
   const int s_lo = singles * x / kNumXcd, s_hi = singles * (x + 1) / kNumXcd;
-  const int u = q / slices, np = p_hi - p_lo, ns = s_hi - s_lo;
-  if (u >= np + ns) return false;
+  const int np = p_hi - p_lo, ns = s_hi - s_lo;
+  const int n = (np + ns) * slices;
+  const int whole = cus > 0 ? n - n % cus : n;  // tiles in whole rounds
+  const int r = n - whole;
+  const int pair_tiles = np * slices;
+  const int busy = whole >= cus && pair_tiles > whole - cus ? pair_tiles - (whole - cus) : 0;
+  int t = q, h = -1;
+  if (r > 0 && 2 * r <= cus - busy && whole >= pair_tiles) {
+    if (q >= whole + 2 * r) return false;
+    if (q >= whole) {
+      t = whole + (q - whole) / 2;
+      h = (q - whole) % 2;
+    }
+  } else if (q >= n) {
+    return false;
+  }
+  const int u = t / slices;
   *single = u >= np;
   *k = uniform(u >= np ? s_lo + u - np : p_lo + u);
-  *slice = uniform(q % slices);
+  *slice = uniform(t % slices);
+  *half = uniform(h);
   return true;
 }
 

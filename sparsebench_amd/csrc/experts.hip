@@ -301,26 +301,31 @@ __global__ void __launch_bounds__(64 * kSddWaves)
 // slices). Every padded row is written, so either DSD tiling may follow.
 using SddPairTile = DmaCfg<256, 256, 32, 4, 2, 4, 0, 2, 5, 1, 1>;
 
-template <class CfgP, class CfgS>
+template <class CfgP, class CfgS, class CfgSH>
 __global__ void __launch_bounds__(CfgP::kThreads)
     sdd_pair_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
                     const int32_t* __restrict__ row_token, const int32_t* __restrict__ tokens_per_expert,
                     const int32_t* __restrict__ padded_offsets, uint16_t* __restrict__ out, int32_t num_tokens,
                     int32_t d_model, int32_t ffn_dim, int32_t num_experts, int32_t max_row_blocks,
-                    int32_t apply_gelu) {
+                    int32_t apply_gelu, int32_t cus_per_xcd) {
   static_assert(CfgP::kThreads == CfgS::kThreads && CfgP::BN == CfgS::BN, "one workgroup and slice width");
-  static_assert(CfgP::BM == 2 * kBS && CfgS::BM == kBS, "pairs and singles of row blocks");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[max_int(CfgP::kLdsAlloc, CfgS::kLdsAlloc)];
-  // Workgroup bid is XCD bid % 8's tile bid / 8 (units x slices, unit-major;
-  // pair_unit_for).
+  static_assert(CfgSH::kThreads == CfgS::kThreads && 2 * CfgSH::BN == CfgS::BN && CfgSH::BK == CfgS::BK,
+                "a single's column halves: same workgroup and K steps");
+  static_assert(CfgP::BM == 2 * kBS && CfgS::BM == kBS && CfgSH::BM == kBS, "pairs and singles of row blocks");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[max_int(CfgP::kLdsAlloc, max_int(CfgS::kLdsAlloc,
+                                                                                         CfgSH::kLdsAlloc))];
+  // Workgroup bid is XCD bid % 8's tile bid / 8 (units x slices, unit-major,
+  // a short last round of singles as column halves; pair_tile_for).
   const int32_t first = expert_counts(tokens_per_expert, num_experts, 0);
   const int live_rb = __builtin_amdgcn_readfirstlane(padded_offsets[num_experts]) / kBS;
   const int slices = ffn_dim / CfgP::BN;
-  if (static_cast<int>(blockIdx.x) / kNumXcd >= pair_units_per_xcd(live_rb) * slices) return;
+  if (static_cast<int>(blockIdx.x) / kNumXcd >= pair_units_per_xcd(live_rb) * slices + cus_per_xcd / 2) return;
   const PairCounts pc = pair_counts(tokens_per_expert, num_experts, first);
   bool single;
-  int k, slice;
-  if (!pair_unit_for(static_cast<int>(blockIdx.x), pc.pairs, pc.singles, slices, &single, &k, &slice)) return;
+  int k, slice, half;
+  if (!pair_tile_for(static_cast<int>(blockIdx.x), pc.pairs, pc.singles, slices, cus_per_xcd, &single, &k, &slice,
+                     &half))
+    return;
   const Chunk ch = find_pair_unit(tokens_per_expert, num_experts, single, k, first);
   // Not a routing layout (the unit would leave the buffers): skip it.
   if (ch.expert < 0 || ch.expert >= num_experts || ch.row0 < 0 || ch.rows < 1 ||
@@ -329,8 +334,10 @@ __global__ void __launch_bounds__(CfgP::kThreads)
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
   if (ch.groups == CfgP::BM / 32)
     sdd_chunk_tile<CfgP>(lds, a, ch, slice * CfgP::BN);
-  else
+  else if (half < 0)
     sdd_chunk_tile<CfgS>(lds, a, ch, slice * CfgS::BN);
+  else
+    sdd_chunk_tile<CfgSH>(lds, a, ch, slice * CfgS::BN + half * CfgSH::BN);
 }
 
 // ------------------------------------------------------------------ DSD ---
@@ -577,15 +584,24 @@ int dispatch_sdd_layer(const void* x, const void* w1, const int32_t* row_token, 
 int launch_sdd_pairs(const void* x, const void* w1, const int32_t* row_token, const int32_t* tokens_per_expert,
                      const int32_t* padded_offsets, void* out, int64_t num_tokens, int64_t d_model, int64_t ffn_dim,
                      int64_t num_experts, int64_t max_row_blocks, int32_t apply_gelu, hipStream_t stream) {
-  if (!reduction_fits<SddPairTile>(d_model) || !reduction_fits<SddNarrowTile>(d_model))
+  if (!reduction_fits<SddPairTile>(d_model) || !reduction_fits<SddNarrowTile>(d_model) ||
+      !reduction_fits<SddNarrowHalfTile>(d_model))
     return fail(SB_ERR_INVALID, "sdd_experts: D (%lld) is not a whole number of the tiles' K steps",
                 static_cast<long long>(d_model));
-  const int64_t grid = int64_t{kNumXcd} * pair_units_per_xcd(static_cast<int>(max_row_blocks)) * (ffn_dim / SddPairTile::BN);
-  sdd_pair_kernel<SddPairTile, SddNarrowTile><<<static_cast<uint32_t>(grid), SddPairTile::kThreads, 0, stream>>>(
-      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, tokens_per_expert, padded_offsets,
-      static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens), static_cast<int32_t>(d_model),
-      static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts), static_cast<int32_t>(max_row_blocks),
-      apply_gelu);
+  int cus = 0;
+  if (const int rc = device_cus(&cus)) return rc;
+  const int cus_per_xcd = cus / kNumXcd;
+  // Each XCD's positions: its tiles, plus up to half its CUs for a split
+  // last round (pair_tile_for).
+  const int64_t grid =
+      int64_t{kNumXcd} *
+      (int64_t{pair_units_per_xcd(static_cast<int>(max_row_blocks))} * (ffn_dim / SddPairTile::BN) + cus_per_xcd / 2);
+  sdd_pair_kernel<SddPairTile, SddNarrowTile, SddNarrowHalfTile>
+      <<<static_cast<uint32_t>(grid), SddPairTile::kThreads, 0, stream>>>(
+          static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w1), row_token, tokens_per_expert,
+          padded_offsets, static_cast<uint16_t*>(out), static_cast<int32_t>(num_tokens),
+          static_cast<int32_t>(d_model), static_cast<int32_t>(ffn_dim), static_cast<int32_t>(num_experts),
+          static_cast<int32_t>(max_row_blocks), apply_gelu, cus_per_xcd);
   return check_launch("sdd_experts");
 }
 

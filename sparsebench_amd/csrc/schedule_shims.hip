@@ -2,7 +2,7 @@
 // over the same __host__ __device__ functions the kernels call
 // (common.hpp: xcd_remap, split_tail, split_tail_slack, tile_coords;
 // expert_chunks.hpp: balanced_chunk_tile, lpt_group_tile, pair_units_per_xcd,
-// pair_unit_for), so tests/test_tile_schedules.py checks the compiled
+// pair_tile_for), so tests/test_tile_schedules.py checks the compiled
 // mappings themselves. Part of the tool library (libsparsebench_probe.so),
 // not of libsparsebench_hip.so's C ABI. No kernel runs.
 
@@ -30,9 +30,10 @@ extern "C" int sbt_balanced_chunk_tile(int bid, int chunks, int slices, int* ran
 
 extern "C" int sbt_pair_units_per_xcd(int units) { return pair_units_per_xcd(units); }
 
-extern "C" int sbt_pair_unit_for(int bid, int pairs, int singles, int slices, int* single, int* k, int* slice) {
+extern "C" int sbt_pair_tile_for(int bid, int pairs, int singles, int slices, int cus, int* single, int* k,
+                                 int* slice, int* half) {
   bool s = false;
-  const bool ok = pair_unit_for(bid, pairs, singles, slices, &s, k, slice);
+  const bool ok = pair_tile_for(bid, pairs, singles, slices, cus, &s, k, slice, half);
   *single = s ? 1 : 0;
   return ok ? 1 : 0;
 }

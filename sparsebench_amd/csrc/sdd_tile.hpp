@@ -138,6 +138,9 @@ __device__ __forceinline__ void sdd_row_block_tile(uint8_t* __restrict__ lds, in
 using SddWideTile = DmaCfg<128, 512, 32, 3, 2, 4, 0, 2, 3, 1, 1>;
 using SddDeepTile = DmaCfg<128, 512, 32, 4, 2, 4, 0, 2, 5, 1, 1>;
 using SddNarrowTile = DmaCfg<128, 256, 64, 3, 2, 4, 0, 2, 3>;
+// Half of the narrow tile (the layer's pair kernel splits a short last round
+// of singles into column halves): the same ring and K steps, 64 x 32 per wave.
+using SddNarrowHalfTile = DmaCfg<128, 128, 64, 3, 2, 4, 0, 2, 3>;
 // Half of a 512-wide tile (the layer kernel splits a short last round of
 // row-block tiles into column halves): 8 waves of 64 x 64, the 4-stage
 // paired ring of the deep tile.

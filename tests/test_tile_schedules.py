@@ -7,7 +7,7 @@ unwritten or written twice without any error on the GPU. These tests walk
 every workgroup id of the launched grid through the mappings the kernels
 call: csrc/common.hpp (xcd_remap, split_tail, split_tail_slack, tile_coords)
 and csrc/expert_chunks.hpp (balanced_chunk_tile, lpt_group_tile,
-pair_units_per_xcd, pair_unit_for) are __host__ __device__ functions, compiled for the CPU into
+pair_units_per_xcd, pair_tile_for) are __host__ __device__ functions, compiled for the CPU into
 the tool library's shims (csrc/schedule_shims.hip), so what is checked here
 is the compiled code, not a restatement of it. What each workgroup must
 cover is stated independently below (the live row blocks, each kind of pair
@@ -44,7 +44,7 @@ def sched():
         ("sbt_tile_coords", None, [i, i, i, i, ip, ip]),
         ("sbt_balanced_chunk_tile", i, [i, i, i, ip, ip]),
         ("sbt_pair_units_per_xcd", i, [i]),
-        ("sbt_pair_unit_for", i, [i, i, i, i, ip, ip, ip]),
+        ("sbt_pair_tile_for", i, [i, i, i, i, i, ip, ip, ip, ip]),
         ("sbt_lpt_group_tile", None, [i, i, i, ctypes.c_uint32, ip, ip]),
     ]:
         fn = getattr(h, name)
@@ -81,23 +81,39 @@ def pair_unit_rows(counts: list[int], single: bool, k: int) -> tuple[int, int]:
     raise AssertionError("unit past the layout")
 
 
-def pair_kernel_tiles(sched, counts: list[int], max_row_blocks: int, slices: int) -> list[tuple[int, int]]:
-    """(row block, slice) of every tile sdd_pair_kernel computes, over its whole grid."""
+def pair_kernel_tiles(sched, counts: list[int], max_row_blocks: int, slices: int,
+                      cus: int = 32) -> list[tuple[int, int, int]]:
+    """(row block, slice, half) of every tile sdd_pair_kernel computes over its whole grid (the
+    launch's size: each XCD's units x slices plus half its CUs); half -1 is the whole slice."""
     live_rb = sum(-(-n // BS) for n in counts if n > 0)
     pairs = sum((-(-n // BS) >> 1) for n in counts if n > 0)
     singles = sum((-(-n // BS) & 1) for n in counts if n > 0)
-    grid = XCD * sched.sbt_pair_units_per_xcd(max_row_blocks) * slices
-    single, k, sl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    grid = XCD * (sched.sbt_pair_units_per_xcd(max_row_blocks) * slices + cus // 2)
+    single, k, sl, half = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     tiles = []
     for bid in range(grid):
-        if bid // XCD >= sched.sbt_pair_units_per_xcd(live_rb) * slices:
+        if bid // XCD >= sched.sbt_pair_units_per_xcd(live_rb) * slices + cus // 2:
             continue  # the kernel's first exit test
-        if not sched.sbt_pair_unit_for(bid, pairs, singles, slices, ctypes.byref(single), ctypes.byref(k),
-                                       ctypes.byref(sl)):
+        if not sched.sbt_pair_tile_for(bid, pairs, singles, slices, cus, ctypes.byref(single), ctypes.byref(k),
+                                       ctypes.byref(sl), ctypes.byref(half)):
             continue
         row0, nrows = pair_unit_rows(counts, bool(single.value), k.value)
-        tiles.extend((r, sl.value) for r in range(row0 // BS, (row0 + nrows) // BS))
+        assert half.value == -1 or (single.value and nrows == BS), "only singles are split"
+        tiles.extend((r, sl.value, half.value) for r in range(row0 // BS, (row0 + nrows) // BS))
+    # Workgroups past the launched grid would be lost: none may have work.
+    for bid in range(grid, grid + 3 * XCD):
+        assert not sched.sbt_pair_tile_for(bid, pairs, singles, slices, cus, ctypes.byref(single), ctypes.byref(k),
+                                           ctypes.byref(sl), ctypes.byref(half))
     return tiles
+
+
+def covered_once(tiles: list[tuple[int, int, int]]) -> list[tuple[int, int]]:
+    """(row block, slice) pairs, each once, from whole tiles or both halves; fails on any overlap."""
+    seen: dict[tuple[int, int], list[int]] = {}
+    for r, s, h in tiles:
+        seen.setdefault((r, s), []).append(h)
+    assert all(v == [-1] or sorted(v) == [0, 1] for v in seen.values()), seen
+    return sorted(seen)
 
 
 def layouts():
@@ -117,24 +133,51 @@ def layouts():
 
 
 @pytest.mark.parametrize("slices", [1, 3, 8])
-def test_pair_kernel_covers_every_live_row_block_once(sched, slices: int) -> None:
+@pytest.mark.parametrize("cus", [32, 38, 10])
+def test_pair_kernel_covers_every_live_row_block_once(sched, slices: int, cus: int) -> None:
     for counts in layouts():
         copies = sum(counts)
         e = len(counts)
         max_rb = (copies + e * (BS - 1)) // BS  # the routing's worst-case sizing
-        tiles = pair_kernel_tiles(sched, counts, max_rb, slices)
+        tiles = pair_kernel_tiles(sched, counts, max_rb, slices, cus)
         live_rb = sum(-(-n // BS) for n in counts if n > 0)
-        assert sorted(tiles) == [(r, s) for r in range(live_rb) for s in range(slices)], counts
+        assert covered_once(tiles) == [(r, s) for r in range(live_rb) for s in range(slices)], counts
+
+
+def test_pair_kernel_splits_only_a_short_last_round_of_singles(sched) -> None:
+    # Per XCD: n tiles on `cus` CUs, r = n % cus in the last round; split iff
+    # those r tiles are all singles and 2r CUs are free for their halves: cus
+    # less the pair tiles still running from the round before.
+    single, k, sl, half = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    for pairs, singles, slices, cus in [(0, 330 // 3, 3, 32), (114, 101, 3, 32), (16, 20, 3, 32), (0, 5, 3, 32),
+                                        (80, 8, 3, 32), (0, 64, 1, 32), (7, 300, 2, 38), (10, 122, 3, 32),
+                                        (1, 109, 3, 32), (100, 180, 3, 32)]:
+        for x in range(XCD):
+            np_ = pairs * (x + 1) // XCD - pairs * x // XCD
+            ns = singles * (x + 1) // XCD - singles * x // XCD
+            n = (np_ + ns) * slices
+            r = n % cus
+            whole = n - r
+            busy = max(0, np_ * slices - (whole - cus)) if whole >= cus else 0
+            split = r > 0 and 2 * r <= cus - busy and whole >= np_ * slices
+            halves = 0
+            for q in range(n + cus):
+                if sched.sbt_pair_tile_for(q * XCD + x, pairs, singles, slices, cus, ctypes.byref(single),
+                                           ctypes.byref(k), ctypes.byref(sl), ctypes.byref(half)):
+                    halves += half.value >= 0
+            assert halves == (2 * r if split else 0), (pairs, singles, slices, cus, x)
 
 
 def test_pair_kernel_xcds_share_each_kind_evenly(sched) -> None:
     # Each XCD's pairs and singles are within one unit of an eighth of each kind.
-    single, k, sl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    single, k, sl, half = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     for pairs, singles in [(114, 101), (0, 7), (5, 0), (31, 1), (1000, 3)]:
-        per = [[0, 0] for _ in range(XCD)]
-        for bid in range(XCD * sched.sbt_pair_units_per_xcd(pairs + singles)):
-            if sched.sbt_pair_unit_for(bid, pairs, singles, 1, ctypes.byref(single), ctypes.byref(k), ctypes.byref(sl)):
-                per[bid % XCD][single.value] += 1
+        units = [set() for _ in range(XCD)]
+        for bid in range(XCD * (sched.sbt_pair_units_per_xcd(pairs + singles) + 16)):
+            if sched.sbt_pair_tile_for(bid, pairs, singles, 1, 32, ctypes.byref(single), ctypes.byref(k),
+                                       ctypes.byref(sl), ctypes.byref(half)):
+                units[bid % XCD].add((single.value, k.value))
+        per = [[sum(1 for kind, _ in u if kind == c) for c in (0, 1)] for u in units]
         assert sum(p for p, _ in per) == pairs and sum(s for _, s in per) == singles
         assert max(p for p, _ in per) - min(p for p, _ in per) <= 1
         assert max(s for _, s in per) - min(s for _, s in per) <= 1

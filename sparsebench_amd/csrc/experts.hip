@@ -36,7 +36,9 @@
 // cost about 10 us each (every workgroup holds up to 160 KB of LDS while it
 // reads the counts). The row-block tiles run on the expert tiles' own code
 // (sdd_chunk_tile / dsd_chunk_tile with the row block as a 128-row chunk,
-// every row read and written), which also needs fewer dependent loads
+// every row read and written, except that the 4-wave DSD reads and writes
+// only the real 32-row groups of an expert of one row block), which also
+// needs fewer dependent loads
 // before the first DMA than the per-row-block kernels' tiles. Next to the
 // expert tiles in one kernel, dsd_row_block_tile's main loop gets a full
 // vmcnt(0) after every step's barrier from the compiler (its LDS-DMA alias
@@ -76,6 +78,11 @@ struct Tag {
 template <int R, int BN, int WAVES, int STAGES>
 using DsdCfg = DmaCfg<32 * R, BN, 32, STAGES, (WAVES == 8 && R % 2 == 0) ? 2 : 1,
                       (WAVES == 8 && R % 2 == 0) ? WAVES / 2 : WAVES, 0, 2, 5, 1, STAGES == 4 ? 1 : 0>;
+
+// A one-row tile configuration cut to R row groups.
+template <class Cfg, int R>
+using RowsCfg = DmaCfg<32 * R, Cfg::BN, Cfg::BK, Cfg::STAGES, Cfg::WM, Cfg::WN, Cfg::CPA, Cfg::CPB, Cfg::PIPE,
+                       Cfg::EPI_PARTS, Cfg::APAIR ? 1 : 0, Cfg::BSTAGES == Cfg::STAGES ? 0 : Cfg::BSTAGES>;
 
 // LDS of the expert tiles of a kernel: the largest over its tile heights.
 template <int BN, int WAVES, int STAGES, int R>
@@ -411,9 +418,12 @@ __device__ __forceinline__ void dsd_chunk_tile(uint8_t* __restrict__ lds, const 
 
 // Expert tiles of the DSD: 4 waves, 256 columns, chunks of up to 256 rows.
 // Row-block tiles: 4 waves, 128 x CfgB::BN, every row of the row block read
-// and written, as sb_dsd's default tile does; they run on the same tile
-// code as the expert chunks (one H buffer, K steps through the row block's
-// own F/128 blocks, as the routing layout stores them).
+// and written, as sb_dsd's default tile does, except for an expert of one
+// row block, whose tile stops at its last real 32-row group (with few
+// tokens most row blocks are such experts, and mostly padding: 93% of the
+// rows at T = 512 of config 5); they run on the same tile code as the
+// expert chunks (one H buffer, K steps through the row block's own F/128
+// blocks, as the routing layout stores them).
 
 template <class CfgB, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES)
@@ -449,11 +459,31 @@ __global__ void __launch_bounds__(64 * WAVES)
     if (rb >= blocks || rb >= max_row_blocks) return;
     const int32_t expert = __builtin_amdgcn_readfirstlane(row_block_expert[rb]);
     if (expert < 0 || expert >= num_experts) return;
-    const Chunk ch{expert, rb * kBS, kBS, 4};
-    if (tt.half < 0)
-      dsd_chunk_tile<CfgB>(lds, a, ch, slice * CfgB::BN);
-    else
-      dsd_chunk_tile<CfgH>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
+    Chunk ch{expert, rb * kBS, kBS, 4};
+    if constexpr (WAVES == 4) {
+      // An expert of one row block: its real 32-row groups only. No other
+      // row block shares its W2 slice, so its tile running ahead of the
+      // others costs no L2 sharing (skipping padding rows in every row
+      // block was slower at the fine-grained shape for that reason). The
+      // padding rows of y are then left unwritten; nothing reads them.
+      const int32_t n = __builtin_amdgcn_readfirstlane(tokens_per_expert[expert]);
+      if (n > 0 && n < kBS) {
+        ch.rows = n;
+        ch.groups = (n + 31) / 32;
+      }
+      with_groups<4>(ch.groups, [&](auto rc) {
+        constexpr int R = decltype(rc)::value;
+        if (tt.half < 0)
+          dsd_chunk_tile<RowsCfg<CfgB, R>>(lds, a, ch, slice * CfgB::BN);
+        else
+          dsd_chunk_tile<RowsCfg<CfgH, R>>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
+      });
+    } else {
+      if (tt.half < 0)
+        dsd_chunk_tile<CfgB>(lds, a, ch, slice * CfgB::BN);
+      else
+        dsd_chunk_tile<CfgH>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
+    }
     return;
   }
   const int chunks = sum.chunks_a;

@@ -129,7 +129,9 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
  * chunk before it) instead of once per row block, and padding rows past
  * the last 32-row group are neither computed nor read. For F % 512 != 0
  * sb_sdd_experts tiles each expert's row blocks in pairs (256 x 256 tiles,
- * an odd last one alone) and writes every padded row, as sb_sdd does. It
+ * an odd last one alone) and writes every padded row, as sb_sdd does,
+ * except, when F < 8192, rows past the first 64 of an expert of at most 64
+ * rows (the DSD's row-block tiles do not read them). It
  * calls sb_sdd itself when x or one expert's W1 is 2 GiB or more (the layer
  * kernels address them with 32-bit offsets).
  * The layout arrays are sb_routing's outputs (or those of

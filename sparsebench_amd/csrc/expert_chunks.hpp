@@ -268,8 +268,9 @@ __device__ __forceinline__ Chunk find_single_chunk_by_size(const int32_t* __rest
 // expert's row blocks two by two from its first, an odd last one alone. A
 // pair is 256 padded rows (8 row groups), a single 128 (4); the tile
 // computes every padded row, so padding rows come out as zeros, as from the
-// per-row-block kernel. Units are numbered in expert order, pairs and
-// singles each counted on their own.
+// per-row-block kernel (a single of an expert of at most 64 rows stops at
+// its first 64 when the DSD's row-block tiles read no further). Units are
+// numbered in expert order, pairs and singles each counted on their own.
 struct PairCounts {
   int32_t pairs, singles;
 };

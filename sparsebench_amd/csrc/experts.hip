@@ -236,8 +236,10 @@ __global__ void __launch_bounds__(64 * kSddWaves)
   if (!(expert_stage_runs(sum, num_experts, kGateSdd, force, ffn_dim / kSddBN, cus_per_xcd * kNumXcd) &&
         dsd_expert)) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in
-    // order; every row is computed and written (padding rows read as zeros).
-    // The tiles of a short last round run as column halves (split_tail).
+    // order; every row is computed and written (padding rows read as zeros),
+    // except past the last 32-row group of an expert of at most 96 rows when
+    // the 4-wave DSD follows, which reads no further. The tiles of a short
+    // last round run as column halves (split_tail).
     const int blocks = sum.chunks_b;
     const int slices = ffn_dim / CfgB::BN;
     const TailTile tt = split_tail(static_cast<int>(blockIdx.x), blocks * slices, cus_per_xcd);
@@ -247,7 +249,26 @@ __global__ void __launch_bounds__(64 * kSddWaves)
     if (rb >= blocks || rb >= max_row_blocks) return;
     const int32_t expert = __builtin_amdgcn_readfirstlane(row_block_expert[rb]);
     if (expert < 0 || expert >= num_experts) return;
-    const Chunk ch{expert, rb * kBS, kBS, 4};
+    Chunk ch{expert, rb * kBS, kBS, 4};
+    const int32_t n = __builtin_amdgcn_readfirstlane(tokens_per_expert[expert]);
+    if (ffn_dim < kDsdDeepF && n > 0 && n <= 3 * 32) {
+      // An expert of one row block whose 4-wave DSD reads its real 32-row
+      // groups only: compute and write those.
+      ch.rows = n;
+      ch.groups = (n + 31) / 32;
+      if (tt.half < 0) {
+        with_groups<3>(ch.groups, [&](auto rc) {
+          sdd_chunk_tile<SddChunkCfg<decltype(rc)::value>>(lds, a, ch, slice * CfgB::BN);
+        });
+      } else if (ch.groups <= 2) {
+        ch.groups = 2;
+        sdd_chunk_tile<RowsCfg<CfgH, 2>>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
+      } else {
+        ch.groups = 4;
+        sdd_chunk_tile<CfgH>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
+      }
+      return;
+    }
     if (tt.half < 0)
       sdd_chunk_tile<CfgB>(lds, a, ch, slice * CfgB::BN);
     else
@@ -305,7 +326,7 @@ __global__ void __launch_bounds__(64 * kSddWaves)
 // runs its pairs, then its singles, so the tiles handed to the CUs that
 // free up last are the short ones; a unit's slices run side by side
 // (sharing its x rows), and so do an expert's pairs (sharing its W1
-// slices). Every padded row is written, so either DSD tiling may follow.
+// slices). Every padded row that a DSD tiling reads is written.
 using SddPairTile = DmaCfg<256, 256, 32, 4, 2, 4, 0, 2, 5, 1, 1>;
 
 template <class CfgP, class CfgS, class CfgSH>
@@ -339,12 +360,27 @@ __global__ void __launch_bounds__(CfgP::kThreads)
       ch.row0 + 32 * ch.groups > max_row_blocks * kBS)
     return;
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
-  if (ch.groups == CfgP::BM / 32)
+  if (ch.groups == CfgP::BM / 32) {
     sdd_chunk_tile<CfgP>(lds, a, ch, slice * CfgP::BN);
-  else if (half < 0)
+    return;
+  }
+  // A single of an expert of one row block of at most 64 rows, whose 4-wave
+  // DSD reads its real 32-row groups only: its first two groups.
+  const int32_t n = __builtin_amdgcn_readfirstlane(tokens_per_expert[ch.expert]);
+  const bool cut = ffn_dim < kDsdDeepF && n > 0 && n <= 64;
+  if (cut) {
+    Chunk c2 = ch;
+    c2.rows = n;
+    c2.groups = 2;
+    if (half < 0)
+      sdd_chunk_tile<RowsCfg<CfgS, 2>>(lds, a, c2, slice * CfgS::BN);
+    else
+      sdd_chunk_tile<RowsCfg<CfgSH, 2>>(lds, a, c2, slice * CfgS::BN + half * CfgSH::BN);
+  } else if (half < 0) {
     sdd_chunk_tile<CfgS>(lds, a, ch, slice * CfgS::BN);
-  else
+  } else {
     sdd_chunk_tile<CfgSH>(lds, a, ch, slice * CfgS::BN + half * CfgSH::BN);
+  }
 }
 
 // ------------------------------------------------------------------ DSD ---

@@ -101,6 +101,21 @@ def real_rows(topo) -> np.ndarray:
     return np.concatenate([np.arange(off[e], off[e] + cnt[e]) for e in range(len(cnt))]).astype(np.int64)
 
 
+def dsd_read_rows(topo, f: int) -> np.ndarray:
+    """Padded rows that a row-block DSD reads: every row of every live row block, except that
+    the 4-wave DSD (F < 8192) reads an expert of one row block (at most 127 rows) only up to its
+    last real 32-row group. A row-block SDD writes at least these."""
+    cnt = topo.tokens_per_expert.cpu().tolist()
+    off = topo.padded_offsets.cpu().tolist()
+    out = []
+    for e, n in enumerate(cnt):
+        if n <= 0:
+            continue
+        end = off[e] + 32 * (-(-n // 32)) if f < 8192 and n < 128 else off[e + 1]
+        out.extend(range(off[e], end))
+    return np.asarray(out, dtype=np.int64)
+
+
 def chunk_pad_rows(topo, rmax: int) -> np.ndarray:
     """Padding rows that the expert kernels write (zeros): up to each last chunk's next multiple of 32."""
     rows_full = 128 * ((32 * rmax) // 128)
@@ -325,9 +340,9 @@ def gate_rule(counts: list[int], stage: str, max_rb: int, d: int, f: int, cus: i
 @pytest.mark.parametrize("case", list(CASES))
 def test_device_choice_follows_the_rule(case: str) -> None:
     # The two paths leave different marks in a NaN-filled output: the
-    # row-block kernels write every row of every live row block, the expert
-    # tiles leave padding rows past an expert's last 32-row group (SDD) or
-    # every padding row (DSD) untouched.
+    # row-block kernels write every row of the row blocks of an expert of
+    # more than one row block, the expert tiles leave padding rows past an
+    # expert's last 32-row group (SDD) or every padding row (DSD) untouched.
     from sparsebench_amd._lib import check, lib, stream_of
     from sparsebench_amd.routing import route_device
 
@@ -352,10 +367,12 @@ def test_device_choice_follows_the_rule(case: str) -> None:
         stream_of(xc.device)))
     torch.cuda.synchronize()
     off = topo.padded_offsets.cpu().tolist()
-    # Padding rows inside live row blocks, past each expert's last 32-row group.
-    untouched = [r for ex, n in enumerate(counts) if n > 0
+    # Padding rows inside live row blocks, past each expert's last 32-row
+    # group, of the experts of more than one row block (the row-block tiles
+    # of an expert of one row block may stop at its last 32-row group too).
+    untouched = [r for ex, n in enumerate(counts) if n > 128
                  for r in range(off[ex] + 32 * (-(-n // 32)), off[ex + 1])]
-    pad = [r for ex, n in enumerate(counts) for r in range(off[ex] + n, off[ex + 1])]
+    pad = [r for ex, n in enumerate(counts) if n > 128 for r in range(off[ex] + n, off[ex + 1])]
     dense = dense_rows(h, fb)
     if f % 512 == 0 and untouched:
         sdd_expert = bool(torch.isnan(dense[torch.tensor(untouched, device="cuda")]).all())
@@ -366,10 +383,11 @@ def test_device_choice_follows_the_rule(case: str) -> None:
 
 
 @pytest.mark.parametrize("case", ["zipf130", "skewed", "pairs768", "uniform768", "one_expert768", "tiny768"])
-def test_sdd_pairs_write_every_row_of_every_live_row_block(case: str) -> None:
-    # F % 512 != 0: the row-block pairs compute whole row blocks, so a
-    # NaN-filled H comes back with zeros on every padding row, as from the
-    # per-row-block kernel, and either DSD tiling may read it.
+def test_sdd_pairs_write_every_row_the_dsd_reads(case: str) -> None:
+    # F % 512 != 0: the row-block pairs compute whole row blocks (a single
+    # of an expert of at most 64 rows its first two 32-row groups), so a
+    # NaN-filled H comes back with zeros on every padding row that either
+    # DSD tiling reads, as from the per-row-block kernel.
     from sparsebench_amd._lib import check, lib, stream_of
     from sparsebench_amd.routing import route_device
 
@@ -386,12 +404,12 @@ def test_sdd_pairs_write_every_row_of_every_live_row_block(case: str) -> None:
         topo.row_offsets.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
         h.data_ptr(), xc.shape[0], d, f, e, max_rb, 1, stream_of(xc.device)))
     torch.cuda.synchronize()
-    live = int(topo.padded_offsets[-1])
     dense = dense_rows(h, fb)
-    assert not torch.isnan(dense[:live]).any(), "every row of every live row block is written"
+    read = torch.as_tensor(dsd_read_rows(topo, f), device="cuda")
+    assert not torch.isnan(dense[read]).any(), "every row the DSD reads is written"
     real = torch.zeros(max_rb * 128, dtype=torch.bool, device="cuda")
     real[torch.as_tensor(real_rows(topo), device="cuda")] = True
-    assert torch.all(dense[:live][~real[:live]] == 0), "padding rows are zeros"
+    assert torch.all(dense[read][~real[read]] == 0), "padding rows are zeros"
 
 
 def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(hooks) -> None:
@@ -425,8 +443,8 @@ def test_sdd_keeps_row_blocks_when_the_dsd_grid_cannot_hold_its_expert_tiles(hoo
         topo.row_offsets.data_ptr(), topo.tokens_per_expert.data_ptr(), topo.padded_offsets.data_ptr(),
         h.data_ptr(), t, d, f, e, max_rb, 1, stream_of(x.device)))
     torch.cuda.synchronize()
-    live = int(topo.padded_offsets[-1])
-    assert not torch.isnan(dense_rows(h, fb)[:live]).any(), "every row of every live row block is written"
+    read = torch.as_tensor(dsd_read_rows(topo, f), device="cuda")
+    assert not torch.isnan(dense_rows(h, fb)[read]).any(), "every row the row-block DSD reads is written"
     gates = torch.ones(t, 1, device="cuda")
     hooks.stage(expert_tiles=False)
     ref = moe_forward(x, idx, gates, w1, w2)

@@ -120,8 +120,8 @@ int sb_dsd(const void* blocks, const void* w, const int32_t* row_offsets, const 
  * enqueues one kernel whose workgroups choose, on the GPU and all alike from
  * tokens_per_expert, between tiles that follow each expert's real rows and
  * row-block tiles of sb_sdd's / sb_dsd's default shape. The DSD's expert
- * tiles run when no expert holds more than twice the mean rows and the
- * DSD's grid holds them; the SDD's run when the DSD's do and either the
+ * tiles run when no expert holds more than twice the mean rows, F >= 1536
+ * and the DSD's grid holds them; the SDD's run when the DSD's do and either the
  * experts hold at most 256 rows on average or the expert tiles need fewer
  * rounds over the device's CUs than the row blocks. An expert's weights
  * are then streamed once per chunk of up to 192 rows (SDD) or 256 rows

@@ -397,7 +397,8 @@ __host__ __device__ __forceinline__ bool balanced_chunk_tile(int bid, int chunks
 // blocks. Every workgroup of the stage's kernel makes the same choice from
 // the same counts, so it costs no host sync.
 //   kGateDsd  expert tiles when the routing is balanced: no expert holds
-//             more than twice the mean rows. Skewed routing keeps row
+//             more than twice the mean rows (and, checked by the layer
+//             kernels next to this gate, F >= 1536). Skewed routing keeps row
 //             blocks: their tiles are all one size, and the many row blocks
 //             of a popular expert run side by side and share its W2 lines
 //             in L2, where chunks of very different sizes leave CUs idle.

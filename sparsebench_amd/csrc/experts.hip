@@ -184,7 +184,13 @@ __device__ __forceinline__ void sdd_chunk_tile(uint8_t* __restrict__ lds, const 
 // before it (tiles of up to 320 rows; with 4 waves the 320 accumulators of
 // such a tile spill). The SDD's choice follows the DSD's, so both are
 // needed here.
-constexpr int kDsdBN = 256, kDsdStages = 4, kDsdDeepF = 8192;
+// The DSD's expert tiles need a reduction of at least kDsdExpertMinF (48
+// K steps): over shorter ones the 256 x 256 tile's fixed costs (ring fill,
+// a 256-row epilogue) outweigh the W2 traffic it saves, and the 128 x 512
+// row-block tiles are faster even with balanced routing (F = 768: 187.1
+// against 160.3 us at T = 16384; F = 1024: 116.6 against 102.5 us at
+// T = 8192, D = 2048), while from F = 1536 on they are even or slower.
+constexpr int kDsdBN = 256, kDsdStages = 4, kDsdDeepF = 8192, kDsdExpertMinF = 1536;
 template <int WAVES>
 constexpr int dsd_rmax() { return WAVES == 8 ? 10 : 8; }
 
@@ -228,11 +234,12 @@ __global__ void __launch_bounds__(64 * kSddWaves)
       summarize_layout<kSddRmax, 4, dsd_rmax<4>(), dsd_rmax<8>()>(tokens_per_expert, num_experts, first);
   const SddArgs a{x, w1, row_token, out, num_tokens, d_model, ffn_dim, apply_gelu};
   // The DSD's own choice (dsd_layer_kernel): its expert tiles when the
-  // routing is balanced and its grid of dsd_grid workgroups holds them all.
-  const bool dsd_expert = force == 1 || (expert_stage_runs(sum, num_experts, kGateDsd, force) &&
-                                         static_cast<int64_t>(ffn_dim >= kDsdDeepF ? sum.chunks_d : sum.chunks_c) *
-                                                 (d_model / kDsdBN) <=
-                                             dsd_grid);
+  // routing is balanced, F >= kDsdExpertMinF and its grid of dsd_grid
+  // workgroups holds them all.
+  const bool dsd_expert =
+      force == 1 || (ffn_dim >= kDsdExpertMinF && expert_stage_runs(sum, num_experts, kGateDsd, force) &&
+                     static_cast<int64_t>(ffn_dim >= kDsdDeepF ? sum.chunks_d : sum.chunks_c) * (d_model / kDsdBN) <=
+                         dsd_grid);
   if (!(expert_stage_runs(sum, num_experts, kGateSdd, force, ffn_dim / kSddBN, cus_per_xcd * kNumXcd) &&
         dsd_expert)) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in
@@ -480,10 +487,12 @@ __global__ void __launch_bounds__(64 * WAVES)
   if (static_cast<int>(blockIdx.x) >= live_rb * (d_model / kDsdBN) + tail_slack) return;
   const LayoutSummary sum = summarize_layout<kRmax, 4>(tokens_per_expert, num_experts, first);
   const DsdArgs a{h, w2, out, h_bytes, ffn_dim, d_model};
-  // The grid may hold fewer workgroups than expert tiles (see the launch):
-  // then the row blocks take the stage.
+  // Expert tiles for balanced routing over a reduction of at least
+  // kDsdExpertMinF. The grid may hold fewer workgroups than expert tiles
+  // (see the launch): then the row blocks take the stage.
   const bool fits = static_cast<int64_t>(sum.chunks_a) * (d_model / kDsdBN) <= static_cast<int64_t>(tile_grid);
-  if (!(expert_stage_runs(sum, num_experts, kGateDsd, force) && (fits || force == 1))) {
+  const bool chosen = ffn_dim >= kDsdExpertMinF && expert_stage_runs(sum, num_experts, kGateDsd, force) && fits;
+  if (!(chosen || force == 1)) {
     // Row blocks: the chunks of up to 128 rows are the live row blocks, in order.
     // The tiles of a short last round run as column halves (split_tail).
     const int blocks = sum.chunks_b;

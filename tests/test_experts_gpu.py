@@ -319,16 +319,16 @@ def dsd_chunks(counts: list[int], f: int) -> int:
 
 
 def gate_rule(counts: list[int], stage: str, max_rb: int, d: int, f: int, cus: int = 256) -> bool:
-    """The choice stated in expert_chunks.hpp, restated: the DSD takes expert
-    tiles iff no expert holds more than twice the mean rows and its grid
-    holds all of them; the SDD iff the DSD does and, besides, the mean is at
+    """The choice stated in expert_chunks.hpp and experts.hip, restated: the DSD
+    takes expert tiles iff no expert holds more than twice the mean rows, F is
+    at least 1536 and its grid holds all of them; the SDD iff the DSD does and, besides, the mean is at
     most 256 rows or its expert chunks (128 rows, a last piece of up to 64
     joined) fill fewer rounds of 512-wide tiles over the CUs than the row
     blocks."""
     counts = [max(c, 0) for c in counts]
     total, most, e = sum(counts), max(counts), len(counts)
     balanced = total > 0 and most * e <= 2 * total
-    dsd = balanced and dsd_chunks(counts, f) * (d // 256) <= dsd_grid(max_rb, e, d)
+    dsd = balanced and f >= 1536 and dsd_chunks(counts, f) * (d // 256) <= dsd_grid(max_rb, e, d)
     if stage == "dsd" or not dsd:
         return dsd
     slices = f // 512

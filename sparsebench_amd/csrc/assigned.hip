@@ -158,16 +158,13 @@ __global__ void __launch_bounds__(256)
     combine_assigned_kernel(const uint16_t* __restrict__ y, const int32_t* __restrict__ copy_row,
                             const G* __restrict__ weights, const int32_t* __restrict__ offsets,
                             const int32_t* __restrict__ copies, uint16_t* __restrict__ out, int64_t num_tokens,
-                            int32_t chunks_per_row, int64_t y_rows, const int32_t* __restrict__ valid_tokens,
-                            Divider div) {
+                            int32_t chunks_per_row, int64_t y_rows, const int32_t* __restrict__ valid_tokens) {
   // Products rounded, then added (no fused multiply-add), as the reference's
   // index_add_ of rows.float() * weight.
 #pragma clang fp contract(off)
-  // Every item number is below 2^31 (checked at the launch).
-  const uint32_t item = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t t32 = divide(item, div);
-  const int64_t t = t32;
-  const int32_t ch = static_cast<int32_t>(item - t32 * static_cast<uint32_t>(chunks_per_row));
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t t = item / chunks_per_row;
+  const int32_t ch = static_cast<int32_t>(item % chunks_per_row);
   const int64_t limit = valid_tokens ? min(num_tokens, static_cast<int64_t>(*valid_tokens)) : num_tokens;
   if (t >= limit) return;
   const int64_t d_model = static_cast<int64_t>(chunks_per_row) * 8;
@@ -199,8 +196,7 @@ int launch_combine_assigned(const void* y, const int32_t* copy_row, const void* 
   const int64_t groups = (num_tokens * chunks + 255) / 256;
   combine_assigned_kernel<G><<<static_cast<uint32_t>(groups), 256, 0, stream>>>(
       static_cast<const uint16_t*>(y), copy_row, static_cast<const G*>(weights), offsets, copies,
-      static_cast<uint16_t*>(out), num_tokens, chunks, y_rows, valid_tokens,
-      make_divider(static_cast<uint32_t>(chunks)));
+      static_cast<uint16_t*>(out), num_tokens, chunks, y_rows, valid_tokens);
   return check_launch("combine (assigned)");
 }
 
@@ -239,7 +235,7 @@ extern "C" int sb_combine_assigned(const void* y, const int32_t* copy_row, const
   if (num_tokens == 0) return clear_ok();
   if (!y || !copy_row || !weights || !token_offsets || !out) return fail(SB_ERR_INVALID, "combine: null buffer");
   if (!aligned16(y) || !aligned16(out)) return fail(SB_ERR_INVALID, "combine: y and out must be 16-byte aligned");
-  if (num_tokens * (d_model / 8) > 2147483647LL - 255) return fail(SB_ERR_INVALID, "combine: too many tokens");
+  if ((num_tokens * (d_model / 8) + 255) / 256 > 2147483647LL) return fail(SB_ERR_INVALID, "combine: too many tokens");
   const hipStream_t s = as_stream(stream);
   switch (weight_dtype) {
     case SB_DTYPE_BF16:

@@ -38,15 +38,13 @@ template <typename G, int KMAX>
 __global__ void __launch_bounds__(256)
     combine_kernel(const uint16_t* __restrict__ y, const int32_t* __restrict__ copy_row, const G* __restrict__ gates,
                    uint16_t* __restrict__ out, int64_t num_tokens, int32_t k, int32_t chunks_per_row, int64_t y_rows,
-                   const int32_t* __restrict__ valid_tokens, Divider div) {
+                   const int32_t* __restrict__ valid_tokens) {
   // Products rounded, then added (no fused multiply-add): the reference's
   // rows.float() * weight, then .sum().
 #pragma clang fp contract(off)
-  // Every item number is below 2^31 (checked at the launch).
-  const uint32_t item = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t t32 = divide(item, div);
-  const int64_t t = t32;
-  const int32_t c = static_cast<int32_t>(item - t32 * static_cast<uint32_t>(chunks_per_row));
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t t = item / chunks_per_row;
+  const int32_t c = static_cast<int32_t>(item % chunks_per_row);
   const int64_t limit = valid_tokens ? min(num_tokens, static_cast<int64_t>(*valid_tokens)) : num_tokens;
   if (t >= limit) return;
   const int64_t d_model = static_cast<int64_t>(chunks_per_row) * 8;
@@ -97,10 +95,9 @@ int launch_combine(const void* y, const int32_t* copy_row, const void* gates, vo
   const auto* yp = static_cast<const uint16_t*>(y);
   const auto* gp = static_cast<const G*>(gates);
   auto* op = static_cast<uint16_t*>(out);
-  const Divider div = make_divider(static_cast<uint32_t>(chunks));
   auto run = [&](auto kmax) {
     combine_kernel<G, decltype(kmax)::value>
-        <<<groups, 256, 0, stream>>>(yp, copy_row, gp, op, num_tokens, k, chunks, y_rows, valid_tokens, div);
+        <<<groups, 256, 0, stream>>>(yp, copy_row, gp, op, num_tokens, k, chunks, y_rows, valid_tokens);
   };
   switch (k) {
     case 1: run(std::integral_constant<int, 1>{}); break;
@@ -126,7 +123,7 @@ extern "C" int sb_combine(const void* y, const int32_t* copy_row, const void* ga
   if (num_tokens == 0) return clear_ok();
   if (!y || !copy_row || !gates || !out) return fail(SB_ERR_INVALID, "combine: null buffer");
   if (!aligned16(y) || !aligned16(out)) return fail(SB_ERR_INVALID, "combine: y and out must be 16-byte aligned");
-  if (num_tokens * (d_model / 8) > 2147483647LL - 255) return fail(SB_ERR_INVALID, "combine: too many tokens");
+  if ((num_tokens * (d_model / 8) + 255) / 256 > 2147483647LL) return fail(SB_ERR_INVALID, "combine: too many tokens");
   const hipStream_t s = as_stream(stream);
   switch (gate_dtype) {
     case SB_DTYPE_BF16:

@@ -62,28 +62,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// ------------------------------------------------------------- division ---
-
-// Division of n < 2^31 by d (1 <= d < 2^31) as a multiply and a shift, for
-// kernels that split a flat item number into row and column: with 2^l >= d
-// and m = floor(2^(31 + l) / d) + 1 (at most 33 bits), floor(n m / 2^(31 + l))
-// = floor(n / d), since n m / 2^(31 + l) exceeds n / d by less than
-// 2^31 / 2^(31 + l) <= 1 / d.
-struct Divider {
-  uint64_t m;
-  uint32_t shift;
-};
-
-inline Divider make_divider(uint32_t d) {
-  uint32_t l = 0;
-  while ((uint64_t{1} << l) < d) ++l;
-  return Divider{((uint64_t{1} << (31 + l)) / d) + 1, 31 + l};
-}
-
-__device__ __forceinline__ uint32_t divide(uint32_t n, Divider div) {
-  return static_cast<uint32_t>((static_cast<uint64_t>(n) * div.m) >> div.shift);
-}
-
 // ------------------------------------------------------------ scheduling ---
 
 constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, each with its own L2

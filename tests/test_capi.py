@@ -114,13 +114,14 @@ def test_combine_rejects_gate_dtype(lib) -> None:
     assert "gate dtype" in _err(lib)
 
 
-def test_combines_reject_more_than_2_31_lanes(lib) -> None:
-    # One lane per 16 bytes of output: T * D / 8 must stay below 2^31 - 255.
+def test_combines_reject_more_than_2_31_workgroups(lib) -> None:
+    # One lane per 16 bytes of output, 256 lanes per workgroup: the grid of
+    # ceil(T * D / 8 / 256) workgroups must stay below 2^31.
     buf = ctypes.create_string_buffer(64)
     p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16
-    assert lib.sb_combine(p, p, p, 0, p, 1 << 28, 2, 64, 4, None, None) == 1
+    assert lib.sb_combine(p, p, p, 0, p, 1 << 36, 2, 64, 4, None, None) == 1
     assert "too many tokens" in _err(lib)
-    assert lib.sb_combine_assigned(p, p, p, 0, p, None, p, 1 << 28, 64, 4, None, None) == 1
+    assert lib.sb_combine_assigned(p, p, p, 0, p, None, p, 1 << 36, 64, 4, None, None) == 1
     assert "too many tokens" in _err(lib)
 
 

@@ -107,9 +107,9 @@ def test_bit_exact_to_reference_arithmetic(gate_dtype, k) -> None:
 
 @pytest.mark.parametrize(("num_tokens", "d_model"), [(5000, 24), (701, 1000), (333, 1032), (90, 2040), (70001, 8)])
 def test_any_row_width_bit_exact(num_tokens, d_model) -> None:
-    # Row widths of 3, 125, 129, 255 and 1 16-byte chunks: the kernels split
-    # the flat lane number into token and chunk by a multiply and a shift,
-    # which must give every lane its own (token, chunk) at any width.
+    # Row widths of 3, 125, 129, 255 and 1 16-byte chunks: each lane splits
+    # its flat number into token and chunk, which must give every lane its
+    # own (token, chunk) at any width.
     from sparsebench_amd import _C
     from sparsebench_amd.moe import combine
 

@@ -79,7 +79,8 @@ template <int R, int BN, int WAVES, int STAGES>
 using DsdCfg = DmaCfg<32 * R, BN, 32, STAGES, (WAVES == 8 && R % 2 == 0) ? 2 : 1,
                       (WAVES == 8 && R % 2 == 0) ? WAVES / 2 : WAVES, 0, 2, 5, 1, STAGES == 4 ? 1 : 0>;
 
-// A one-row tile configuration cut to R row groups.
+// A tile configuration cut to R row groups (R a multiple of its rows of
+// waves, WM: DmaCfg asserts that each wave owns whole 32-row groups).
 template <class Cfg, int R>
 using RowsCfg = DmaCfg<32 * R, Cfg::BN, Cfg::BK, Cfg::STAGES, Cfg::WM, Cfg::WN, Cfg::CPA, Cfg::CPB, Cfg::PIPE,
                        Cfg::EPI_PARTS, Cfg::APAIR ? 1 : 0, Cfg::BSTAGES == Cfg::STAGES ? 0 : Cfg::BSTAGES>;
@@ -268,6 +269,7 @@ __global__ void __launch_bounds__(64 * kSddWaves)
           sdd_chunk_tile<SddChunkCfg<decltype(rc)::value>>(lds, a, ch, slice * CfgB::BN);
         });
       } else if (ch.groups <= 2) {
+        // The half tile's two rows of waves take an even number of groups.
         ch.groups = 2;
         sdd_chunk_tile<RowsCfg<CfgH, 2>>(lds, a, ch, slice * CfgB::BN + tt.half * CfgH::BN);
       } else {

@@ -83,6 +83,9 @@ CASES = {
     "one_expert768": (lambda s: torch.zeros(3000, 1, dtype=torch.int64), 1, 256, 768),
     # Five tokens over three experts at F = 768 (singles only, a grid of a few workgroups).
     "tiny768": (lambda s: torch.tensor([[0], [2], [2], [0], [2]], dtype=torch.int64), 3, 256, 768),
+    # F = 1536, the shortest reduction on which the DSD may take its expert
+    # tiles (kDsdExpertMinF); 256 rows per expert on average.
+    "uniform1536": (lambda s: routing_case("random", 2048, 16, seed=s), 16, 256, 1536),
 }
 
 # SDD-only cases (D % 256 != 0 leaves the DSD's layer tiles out): short
